@@ -1,0 +1,173 @@
+/*
+ * lazykv_hip.h -- C ABI of the MI355X (gfx950) tiered decode-attention hot path.
+ *
+ * Each entry point replaces a function (or a fused chain of torch ops) that the reference's
+ * Python drives; the reference file:line is given beside each declaration (paths relative to the
+ * LazyKV repository root). Conventions shared by every function:
+ *
+ *  - Plain pointers and sizes only. Device pointers may point into HBM or be the device alias of
+ *    mapped pinned host memory (lkv_host_alloc): a kernel reading the latter reads host RAM over
+ *    PCIe in place.
+ *  - `stream` is a hipStream_t passed as an integer (0 = the null stream). Work is enqueued only:
+ *    no entry point synchronises the stream, and none allocates device memory. Scratch space is
+ *    the caller's `ws` buffer, sized by the matching *_workspace_bytes function; it must be zeroed
+ *    once before its first use and is left zeroed by every successful kernel (arrival counters
+ *    reset themselves), so it can be reused across calls on one stream. Calls that overlap on
+ *    different streams need distinct workspaces.
+ *  - Return value: LKV_OK (0) or a negative LKV_ERR_*; shapes and arguments are validated before
+ *    any launch. lkv_last_error() returns a message for the calling thread's last failure.
+ *  - Dtype codes: LKV_F16, LKV_BF16, LKV_F32 for model-dtype tensors; LKV_INT8_RECORD for the
+ *    int8 warm/cold records of lazykv/quant.py:46-105 (kq | vq | k scale | k zero | v scale |
+ *    v zero, float16 scales).
+ */
+#ifndef LAZYKV_HIP_H
+#define LAZYKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LKV_OK = 0,
+  LKV_ERR_INVALID = -1, /* bad argument or shape (the reference raises ValueError) */
+  LKV_ERR_HIP = -2,     /* a HIP runtime call or launch failed */
+  LKV_ERR_UNSUPPORTED = -3
+};
+
+enum { LKV_F16 = 0, LKV_BF16 = 1, LKV_F32 = 2, LKV_INT8_RECORD = 3 };
+
+/* lkv_bound_topk flags */
+enum { LKV_SORTED = 1 };
+/* rank modes: the float32 bound (lazykv/selection.py:46-48 with dtype=float32) or the model
+   dtype's rounding points (dtype=None: each product and their sum rounded to the model dtype) */
+enum { LKV_RANK_F32 = 0, LKV_RANK_MODEL = 1 };
+/* lkv_host_alloc flags */
+enum { LKV_HOST_COHERENT = 1 };
+
+/*
+ * Where one set of KV blocks lives. Block b of KV head h has its key rows at
+ *   k + (b * block_stride + h * head_stride) elements, rows head_dim elements apart,
+ * and its value rows at the same offset from `v`. For LKV_INT8_RECORD, `k` points at records,
+ * the strides are in bytes, `v` is unused and `deq_dtype` is the model dtype that dequantised
+ * values are rounded to (lazykv/quant.py:103-105). Blocks 0..n_blocks-1 are addressable: a
+ * kernel skips (attends nothing from) a block id outside that range rather than reading it.
+ * Layouts this describes: the host pool and GPU slot pool [blocks, h, 2, bs, d]
+ * (lazykv/tiered.py:261,265), the int8 host pool [blocks, h, P], a full cache [1, h, T, d]
+ * (lazykv/cache.py:35-36) and the exact tier's float32 mirror [h, T, d] (lazykv/exact.py:131-140).
+ */
+typedef struct lkv_kv_source {
+  const void* k;
+  const void* v;
+  int64_t block_stride;
+  int64_t head_stride;
+  int64_t n_blocks;
+  int32_t dtype;
+  int32_t deq_dtype;
+} lkv_kv_source;
+
+/* Shape and sequence state of one decode-attention call. */
+typedef struct lkv_decode_desc {
+  int32_t n_q;       /* query heads */
+  int32_t n_kv;      /* KV heads; n_q % n_kv == 0 (GQA) */
+  int32_t head_dim;  /* 64 or 128 */
+  int32_t block_size;/* tokens per block; a multiple of 4, at most 64 */
+  float scale;       /* softmax scaling (Llama: head_dim ** -0.5) */
+  int32_t k;         /* entries per KV head in `idx` */
+  int32_t attend_selected; /* 1: attend the idx blocks from `sel`; 0: idx only excludes */
+  int32_t sink_block;/* block id read from `sink`, or -1 for none */
+  int32_t cur_block; /* block id read from `cur`, or -1 for none */
+  int32_t fill;      /* valid tokens of the current block, 1..block_size */
+  int32_t rem_first; /* remainder: blocks [rem_first, rem_last) of `rem` that are not in idx */
+  int32_t rem_last;  /* rem_first == rem_last: no remainder */
+} lkv_decode_desc;
+
+/* ---- errors and version -------------------------------------------------------------------- */
+const char* lkv_last_error(void);
+int lkv_abi_version(void);
+
+/* ---- a12: mapped pinned host memory (lazykv/pinned.py:31-42 pinned_empty, :73-92 device_view)
+ * Exact-size page-locked host memory, mapped into the device address space. The reference
+ * pins an ordinary allocation in place with cudaHostRegister; here the pool is allocated
+ * pinned from the start (hipHostMalloc), which is also exact-size and needs no registration.
+ * flags: LKV_HOST_COHERENT selects fine-grained (uncached on the device) memory; the default
+ * is coarse-grained, which the device may cache between kernel boundaries. */
+int lkv_host_alloc(size_t bytes, int flags, void** host_ptr);
+int lkv_host_free(void* host_ptr);
+int lkv_host_device_pointer(const void* host_ptr, void** dev_ptr);
+
+/* ---- a1 + a2: Quest bound and on-device top-K (lazykv/selection.py:38-62; call sites
+ * lazykv/tiered.py:383-387 rank and :500 gather_zerocopy)
+ * q [n_q, d] (q_dtype); kmin/kmax: block metadata of KV head h, block b at
+ * meta + h*meta_head_stride + b*d (meta_dtype elements). Candidates are blocks
+ * cand_offset .. cand_offset+n_cand-1. Writes, per KV head, the ids (cand_offset included, the
+ * reference's `+ 1`) of the k blocks with the highest bound to out_idx[h*idx_stride + j]:
+ * in descending bound order with LKV_SORTED (ties: lower id first), else in ascending id order.
+ * out_bound, if not NULL, receives the float32 bound [n_kv, n_cand]. k == 0 computes bounds only.
+ * The indices never leave the device. */
+size_t lkv_bound_topk_workspace_bytes(int n_kv, int n_cand, int k);
+int lkv_bound_topk(uintptr_t stream, const void* q, int q_dtype, const void* kmin, const void* kmax, int meta_dtype,
+                   int64_t meta_head_stride, int n_q, int n_kv, int head_dim, int cand_offset, int n_cand, int k,
+                   int rank_mode, int flags, int32_t* out_idx, int64_t idx_stride, float* out_bound, void* ws,
+                   size_t ws_bytes);
+
+/* ---- a5 + a6 + a7 + a9 + a11: block-sparse GQA decode attention with LSE
+ * (lazykv/attention.py:97-136 attend over the set lazykv/tiered.py:489-511 gather_zerocopy
+ * builds; lazykv/exact.py:225-288 merge/_gpu_lse; lazykv/exact.py:88-127 cpu_partial_attention)
+ * Attends one query token per head over, per KV head h: the sink block (from `sink`), the
+ * blocks idx[h*idx_stride + 0..k) (from `sel`, when attend_selected), the current block's
+ * first `fill` tokens (from `cur`), and every block of [rem_first, rem_last) that is not in
+ * idx (from `rem`): the exact tier's cold remainder, merged in the same kernel by log-sum-exp.
+ * `sel` and `rem` may be LKV_INT8_RECORD: their pairs are dequantised inside the load (the sink
+ * and current block stay in the model dtype, lazykv/tiered.py:200-202). Writes
+ * out [n_q, d] (out_dtype) and lse [n_q] (float32, natural log); an empty set gives lse = -inf
+ * and a zero output. sink/cur/rem may be NULL when unused. */
+size_t lkv_sparse_decode_workspace_bytes(const lkv_decode_desc* desc);
+int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
+                      const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride, const lkv_kv_source* sink,
+                      const lkv_kv_source* cur, const lkv_kv_source* rem, void* out, int out_dtype, float* lse,
+                      void* ws, size_t ws_bytes);
+
+/* ---- a8: exact two-partial merge (lazykv/exact.py:69-85 merge_lse)
+ * rows x d outputs (dtype_in) and their LSEs; an empty partial (lse -inf) contributes 0.
+ * out/lse may alias out_a/lse_a. */
+int lkv_merge_lse(uintptr_t stream, const void* out_a, const float* lse_a, const void* out_b, const float* lse_b,
+                  int dtype_in, int64_t rows, int head_dim, void* out, int out_dtype, float* lse);
+
+/* ---- a10 + a11 + a4: int8 pack / unpack and block metadata (lazykv/quant.py:59-105;
+ * lazykv/tiered.py:162-197 boundary, :353-375 seal, :226-236 metadata rebuild)
+ * lkv_store_blocks reads blocks [first_block, first_block+n_blocks) of every KV head from
+ * `src` (model dtype) and, depending on dst->dtype:
+ *   model dtype      -- copies each pair into dst (the seal-time store into the host pool);
+ *   LKV_INT8_RECORD  -- writes the int8 record of each pair (quant.py pack);
+ *   dst == NULL      -- stores nothing.
+ * If kmin/kmax are not NULL, writes the per-channel key min/max of each block to
+ * meta + h*meta_head_stride + b*d (meta_dtype): of the exact keys, or, for an int8 destination,
+ * of the dequantised keys (lazykv/tiered.py:182-194,364-370). src may itself be
+ * LKV_INT8_RECORD only when dst is NULL (metadata from existing records). */
+int lkv_store_blocks(uintptr_t stream, const lkv_kv_source* src, const lkv_kv_source* dst, int n_kv, int head_dim,
+                     int block_size, int first_block, int n_blocks, void* kmin, void* kmax, int meta_dtype,
+                     int64_t meta_head_stride);
+
+/* quant.py pack: pairs [m, 2, bs, d] (dtype) -> records [m, P] (lazykv/quant.py:73-87) */
+int lkv_pack_int8(uintptr_t stream, const void* pairs, int dtype, int64_t m, int block_size, int head_dim,
+                  void* records);
+/* quant.py unpack: records [m, P] -> pairs [m, 2, bs, d] (lazykv/quant.py:90-105) */
+int lkv_unpack_int8(uintptr_t stream, const void* records, int64_t m, int block_size, int head_dim, int dtype,
+                    void* pairs);
+/* packed_pair_bytes (lazykv/quant.py:46-49) */
+int64_t lkv_packed_pair_bytes(int block_size, int head_dim);
+
+/* ---- measurement: a streaming read of `bytes` at `src` (HBM or mapped host memory), the
+ * device-side probe of the link asymptote that the byte roofline uses; no reference
+ * counterpart (the reference quotes a probe figure at configs/phase23.yaml:13). Writes one
+ * checksum word per workgroup to sink[0..blocks). */
+int lkv_stream_read(uintptr_t stream, const void* src, size_t bytes, int blocks, uint32_t* sink);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAZYKV_HIP_H */

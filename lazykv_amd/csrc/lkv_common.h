@@ -1,0 +1,237 @@
+// Shared device helpers and host-side error plumbing for the tiered decode-attention kernels.
+//
+// Target: gfx950 (CDNA4), wave64. Every kernel maps one KV row (head_dim elements) onto 16
+// consecutive lanes, so one wave-wide load instruction covers 4 rows, each row read as one
+// coalesced segment. Cross-lane sums within a 16-lane row use DPP (quad permutes and row
+// mirrors); the 4 row groups of a wave combine through lane swizzles (xor 16 / xor 32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lazykv_hip.h"
+
+// ---------------------------------------------------------------------------------------------
+// Host side: error state shared by every entry point (defined in lkv_api.hip).
+// ---------------------------------------------------------------------------------------------
+void lkv_set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void lkv_clear_error();
+
+#define LKV_CHECK_ARG(cond, ...)          \
+  do {                                    \
+    if (!(cond)) {                        \
+      lkv_set_error(__VA_ARGS__);         \
+      return LKV_ERR_INVALID;             \
+    }                                     \
+  } while (0)
+
+#define LKV_CHECK_HIP(expr)                                                             \
+  do {                                                                                  \
+    hipError_t e_ = (expr);                                                             \
+    if (e_ != hipSuccess) {                                                             \
+      lkv_set_error("%s failed: %s (%d)", #expr, hipGetErrorString(e_), (int)e_);       \
+      return LKV_ERR_HIP;                                                               \
+    }                                                                                   \
+  } while (0)
+
+// Launch-status check: a kernel launch reports configuration errors through hipGetLastError.
+#define LKV_CHECK_LAUNCH(name)                                                          \
+  do {                                                                                  \
+    hipError_t e_ = hipGetLastError();                                                  \
+    if (e_ != hipSuccess) {                                                             \
+      lkv_set_error("%s launch failed: %s (%d)", name, hipGetErrorString(e_), (int)e_); \
+      return LKV_ERR_HIP;                                                               \
+    }                                                                                   \
+  } while (0)
+
+static inline size_t lkv_align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+static inline bool lkv_is_model_dtype(int dt) { return dt == LKV_F16 || dt == LKV_BF16 || dt == LKV_F32; }
+
+static inline int lkv_dtype_size(int dt) { return dt == LKV_F32 ? 4 : (dt == LKV_INT8_RECORD ? 1 : 2); }
+
+// ---------------------------------------------------------------------------------------------
+// Device side.
+// ---------------------------------------------------------------------------------------------
+namespace lkv {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float bits_to_float(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t float_to_bits(float f) { return __float_as_uint(f); }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return bits_to_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return (float)v;
+}
+
+// float32 -> bfloat16 bits, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = float_to_bits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// float32 -> float16 bits, round to nearest even (the hardware conversion's default mode).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  _Float16 h = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// Model-dtype element type tags.
+template <int DT> struct Elem;
+template <> struct Elem<LKV_F16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(T x) { return f16_to_f32(x); }
+  static __device__ __forceinline__ T store(float f) { return f32_to_f16(f); }
+};
+template <> struct Elem<LKV_BF16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(T x) { return bf16_to_f32(x); }
+  static __device__ __forceinline__ T store(float f) { return f32_to_bf16(f); }
+};
+template <> struct Elem<LKV_F32> {
+  using T = float;
+  static __device__ __forceinline__ float load(T x) { return x; }
+  static __device__ __forceinline__ T store(float f) { return f; }
+};
+
+// Round a float32 through a model dtype and widen it back (identity for float32).
+template <int DT>
+__device__ __forceinline__ float round_through(float f) {
+  if constexpr (DT == LKV_F32) {
+    return f;
+  } else {
+    return Elem<DT>::load(Elem<DT>::store(f));
+  }
+}
+
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dt) {
+  if (dt == LKV_F32) return ((const float*)p)[i];
+  uint16_t b = ((const uint16_t*)p)[i];
+  return dt == LKV_BF16 ? bf16_to_f32(b) : f16_to_f32(b);
+}
+
+__device__ __forceinline__ void store_any(void* p, int64_t i, int dt, float v) {
+  if (dt == LKV_F32) {
+    ((float*)p)[i] = v;
+  } else {
+    ((uint16_t*)p)[i] = dt == LKV_BF16 ? f32_to_bf16(v) : f32_to_f16(v);
+  }
+}
+
+// Load N contiguous elements (N * sizeof(T) bytes, naturally aligned) and widen to float.
+template <int DT, int N>
+__device__ __forceinline__ void load_row_segment(const typename Elem<DT>::T* p, float (&out)[N]) {
+  using T = typename Elem<DT>::T;
+  constexpr int BYTES = N * (int)sizeof(T);
+  static_assert(BYTES % 4 == 0 || BYTES == 2, "segment must be dword sized");
+  if constexpr (BYTES == 2) {
+    out[0] = Elem<DT>::load(p[0]);
+  } else {
+    constexpr int WORDS = BYTES / 4;
+    uint32_t w[WORDS];
+    if constexpr (WORDS % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < WORDS / 4; ++i) {
+        uint4 v = ((const uint4*)p)[i];
+        w[4 * i + 0] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+      }
+    } else if constexpr (WORDS == 2) {
+      uint2 v = *(const uint2*)p;
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < WORDS; ++i) w[i] = ((const uint32_t*)p)[i];
+    }
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) out[i] = bits_to_float(w[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) {
+        out[2 * i] = Elem<DT>::load((uint16_t)(w[i] & 0xffffu));
+        out[2 * i + 1] = Elem<DT>::load((uint16_t)(w[i] >> 16));
+      }
+    }
+  }
+}
+
+// ---- cross-lane reductions -------------------------------------------------------------------
+// DPP control words (GFX9): quad permutes, half-row mirror (lane i <-> 7-i within 8),
+// row mirror (lane i <-> 15-i within 16). Pairing lanes this way sums a full 16-lane row in
+// four steps without touching LDS.
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppMirror = 0x140;     // row_mirror
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 16 lanes of a row; every lane of the row receives the total.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<kDppQuadSwap1>(x);
+  x += dpp<kDppQuadSwap2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  x += dpp<kDppMirror>(x);
+  return x;
+}
+
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp<kDppQuadSwap1>(x));
+  x = fmaxf(x, dpp<kDppQuadSwap2>(x));
+  x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppMirror>(x));
+  return x;
+}
+
+__device__ __forceinline__ float row16_min(float x) {
+  x = fminf(x, dpp<kDppQuadSwap1>(x));
+  x = fminf(x, dpp<kDppQuadSwap2>(x));
+  x = fminf(x, dpp<kDppHalfMirror>(x));
+  x = fminf(x, dpp<kDppMirror>(x));
+  return x;
+}
+
+// Combine the four 16-lane row groups of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float xor_lane(float x, int mask) { return __shfl_xor(x, mask, 64); }
+
+__device__ __forceinline__ float groups4_sum(float x) {
+  x += xor_lane(x, 16);
+  x += xor_lane(x, 32);
+  return x;
+}
+__device__ __forceinline__ float groups4_max(float x) {
+  x = fmaxf(x, xor_lane(x, 16));
+  x = fmaxf(x, xor_lane(x, 32));
+  return x;
+}
+__device__ __forceinline__ float groups4_min(float x) {
+  x = fminf(x, xor_lane(x, 16));
+  x = fminf(x, xor_lane(x, 32));
+  return x;
+}
+
+// Release this thread's prior global writes at device scope, then count one arrival on
+// `counter`; returns the previous count. Acquire on the returning side is `acquire_device()`.
+__device__ __forceinline__ void release_device() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void acquire_device() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_counter(uint32_t* counter) {
+  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace lkv

@@ -1,0 +1,398 @@
+"""The tier's decode path on the GPU: TieredLayer / TieredCache counterparts of lazykv/tiered.py.
+
+What a selecting layer does per decode step, with no host synchronisation anywhere:
+
+1. `append` writes the token into the current block's slot; a full block is sealed first by one
+   kernel that stores it into the host pool (as model-dtype bytes or as an int8 record) and
+   writes its key min/max metadata (lazykv/tiered.py:306-314,353-375).
+2. `rank` scores every candidate block (1 .. n_sealed-1) with the Quest bound and selects the top
+   K per KV head on the device (lazykv/tiered.py:383-387, without the `.cpu()`).
+3. `decode` attends sink + selected + current[:fill] in one block-sparse kernel that reads each
+   selected pair where it lives: in place from the mapped host pool over PCIe (`fetch="zerocopy"`,
+   lazykv/tiered.py:489-511) or from an HBM store (`fetch="resident"`, all blocks on the GPU as
+   in rung 5, lazykv/selection.py:147-183). With `exact=True` the same kernel also attends every
+   other sealed block from the host tier and merges the two partials by log-sum-exp
+   (lazykv/exact.py:225-264), so the result is full attention.
+
+Layouts follow the reference: GPU slot pool [2, h, 2, bs, d] holding the sink (slot 0) and the
+current block (slot 1) (`n_slots=0`, lazykv/tiered.py:250,261); host pool [cap, h, 2, bs, d] in
+the model dtype or [cap, h, P] int8 records (:265); metadata [1, h, cap, d] in the model dtype
+(:262), taken over the dequantised keys for an int8 tier (:182-194). The residency machinery of
+rungs 6-7 (slots, admit, prefetch) is not part of this path.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any
+
+import numpy as np
+import torch
+
+from lazykv_amd import _lib, kernels
+from lazykv_amd.pinned import pinned_empty
+from lazykv_amd.quant import packed_pair_bytes
+from lazykv_amd.selection import QUEST_DENSE_LAYERS
+
+FETCH_MODES = ("zerocopy", "resident")
+
+
+@dataclass
+class TierCounters:
+    """Work counters of the tier (lazykv/tiered.py:76-109, the zero-copy and seal fields)."""
+
+    selections: int = 0
+    selected_pairs: int = 0
+    zerocopy_bytes: int = 0
+    remainder_pairs: int = 0
+    seals: int = 0
+    seal_bytes: int = 0
+    boundary_d2h_bytes: int = 0
+    fetched_pairs_per_step: list[int] = field(default_factory=list)
+
+
+@dataclass
+class Decoded:
+    """What `TieredCache.select` returns: the finished attention of the step, not a key set.
+
+    out [1, n_q, 1, d] in the model dtype, lse [1, n_q] float32 (natural log).
+    """
+
+    out: torch.Tensor
+    lse: torch.Tensor
+
+
+def allocate_host_pools(n_layers: int, heads: int, head_dim: int, block_size: int, capacity_tokens: int, dtype: torch.dtype = torch.bfloat16, quant: str | None = None, coherent: bool = False) -> list[torch.Tensor]:
+    """Mapped pinned host pools, one per selecting layer (lazykv/tiered.py:874-882)."""
+    blocks = -(-capacity_tokens // block_size)
+    if quant is None:
+        shape, dt = (blocks, heads, 2, block_size, head_dim), dtype
+    elif quant == "int8":
+        shape, dt = (blocks, heads, packed_pair_bytes(block_size, head_dim)), torch.uint8
+    else:
+        raise ValueError(f"unknown tier precision {quant!r}")
+    return [pinned_empty(shape, dt, coherent=coherent) for _ in range(n_layers)]
+
+
+class TieredLayer:
+    """One selecting layer: slot pool (sink + current), host pool, optional HBM store, metadata."""
+
+    def __init__(
+        self,
+        keys: torch.Tensor,
+        values: torch.Tensor,
+        k_blocks: int,
+        block_size: int,
+        capacity_tokens: int,
+        host: torch.Tensor | None = None,
+        n_slots: int | None = None,
+        quant: str | None = None,
+        fetch: str = "zerocopy",
+        exact: bool = False,
+        rank_dtype: torch.dtype | None = torch.float32,
+    ) -> None:
+        """Build the tier from a prompt's KV [1, h, L, d] on the GPU (lazykv/tiered.py:153-206).
+
+        Every full block is stored to the host pool once and its metadata written, by one kernel;
+        the tail goes to the current slot.
+        """
+        _lib.require_cuda(keys, values)
+        _, h, length, d = keys.shape
+        n_blocks, tail = divmod(length, block_size)
+        self._allocate(h, d, n_blocks, k_blocks, block_size, capacity_tokens, keys.device, keys.dtype, host, n_slots, quant, fetch, exact, rank_dtype)
+        src = kernels.dense_source(keys, values, block_size)
+        self._store(src, 0, n_blocks, with_store=True)
+        self.boundary_d2h_bytes = n_blocks * h * self.pair_bytes if self.host is not None else 0
+        # The sink never leaves VRAM and stays exact even under an int8 tier (lazykv/tiered.py:200-202).
+        self.pool[0, :, 0] = keys[0, :, :block_size]
+        self.pool[0, :, 1] = values[0, :, :block_size]
+        if tail:
+            self.pool[1, :, 0, :tail] = keys[0, :, n_blocks * block_size : length]
+            self.pool[1, :, 1, :tail] = values[0, :, n_blocks * block_size : length]
+        self.n_sealed, self.fill, self.length = n_blocks, tail, length
+
+    @classmethod
+    def from_state(
+        cls,
+        h: int,
+        d: int,
+        k_blocks: int,
+        block_size: int,
+        capacity_tokens: int,
+        device: torch.device,
+        dtype: torch.dtype,
+        host: torch.Tensor | None = None,
+        quant: str | None = None,
+        fetch: str = "zerocopy",
+        exact: bool = False,
+        rank_dtype: torch.dtype | None = torch.float32,
+    ) -> TieredLayer:
+        """An empty layer whose pools the caller fills (`load_blocks`, `set_current`), e.g. a restore."""
+        self = cls.__new__(cls)
+        self._allocate(h, d, capacity_tokens // block_size, k_blocks, block_size, capacity_tokens, device, dtype, host, 0, quant, fetch, exact, rank_dtype, check_budget=False)
+        self.n_sealed, self.fill, self.length = 0, 0, 0
+        self.boundary_d2h_bytes = 0
+        return self
+
+    def _allocate(self, h, d, n_blocks, k_blocks, bs, capacity_tokens, dev, dt, host, n_slots, quant, fetch, exact, rank_dtype, check_budget=True) -> None:  # noqa: ANN001
+        if check_budget and n_blocks - 1 <= k_blocks:
+            raise ValueError(f"budget of {k_blocks} blocks covers all {n_blocks - 1} candidate blocks; the tier needs selection")
+        if n_slots not in (None, 0):
+            raise ValueError("the GPU tier holds only the sink and the current block in slots (n_slots=0)")
+        if quant not in (None, "int8"):
+            raise ValueError(f"unknown tier precision {quant!r}")
+        if fetch not in FETCH_MODES:
+            raise ValueError(f"unknown fetch mode {fetch!r}; expected one of {FETCH_MODES}")
+        if exact and fetch != "resident":
+            raise ValueError("the exact tier attends the selected blocks from HBM: it needs fetch='resident'")
+        if dt not in (torch.float16, torch.bfloat16):
+            raise ValueError(f"KV dtype {dt} unsupported: float16 or bfloat16")
+        self.h, self.d, self.bs, self.k = h, d, bs, k_blocks
+        self.n_slots, self.tail_slot = 0, 1
+        self.quant, self.fetch, self.exact = quant, fetch, exact
+        self.rank_mode = _lib.RANK_F32 if rank_dtype == torch.float32 else _lib.RANK_MODEL
+        self.dtype = dt
+        self.cap_blocks = -(-capacity_tokens // bs)
+        # Zeroed: the current block's unfilled rows are masked (lazykv/tiered.py:259-261).
+        self.pool = torch.zeros((2, h, 2, bs, d), dtype=dt, device=dev)
+        self.kmin = torch.zeros((1, h, self.cap_blocks, d), dtype=dt, device=dev)
+        self.kmax = torch.zeros_like(self.kmin)
+        self.logical_pair_bytes = 2 * bs * d * self.pool.element_size()
+        need_host = fetch == "zerocopy" or exact
+        shape = (self.cap_blocks, h, 2, bs, d) if quant is None else (self.cap_blocks, h, packed_pair_bytes(bs, d))
+        want = dt if quant is None else torch.uint8
+        if host is None and need_host:
+            host = pinned_empty(shape, want)
+        elif host is not None and (tuple(host.shape) != shape or host.dtype != want):
+            raise ValueError(f"host pool must be pinned {want} with shape {shape}, got {host.dtype} {tuple(host.shape)}")
+        self.host = host
+        self.pair_bytes = self.logical_pair_bytes if quant is None else packed_pair_bytes(bs, d)
+        self.store = torch.zeros((self.cap_blocks, h, 2, bs, d), dtype=dt, device=dev) if fetch == "resident" else None
+        self._host_src = None
+        if host is not None:
+            self._host_src = kernels.pool_source(host) if quant is None else kernels.record_source(host, dt)
+        self._store_src = kernels.pool_source(self.store) if self.store is not None else None
+        self._pool_src = kernels.pool_source(self.pool)
+
+    # -- writes ---------------------------------------------------------------------------------
+
+    def _store(self, src: kernels.Source, first: int, n: int, with_store: bool) -> None:
+        """Store blocks [first, first+n) from `src` into the host pool / HBM store, with metadata."""
+        if n <= 0:
+            return
+        if first + n > self.cap_blocks:
+            raise RuntimeError(f"host pool full: {self.cap_blocks} blocks")
+        common = dict(n_kv=self.h, head_dim=self.d, block_size=self.bs)
+        # The metadata comes from the bytes a read will produce: the dequantised keys for an int8
+        # host tier, unless the selected blocks are read from the exact HBM store.
+        meta_from_host = self._host_src is not None and not (self.store is not None)
+        if self._host_src is not None:
+            kernels.store_blocks(src, dst=self._host_src, first_block=first, n_blocks=n,
+                                 kmin=self.kmin if meta_from_host else None, kmax=self.kmax if meta_from_host else None, **common)
+        if self.store is not None and with_store:
+            kernels.store_blocks(src, dst=self._store_src, first_block=first, n_blocks=n, kmin=self.kmin, kmax=self.kmax, **common)
+
+    def load_blocks(self, pairs: torch.Tensor, first: int) -> None:
+        """Store `pairs` [n, h, 2, bs, d] (GPU, model dtype) as blocks first..first+n-1 (boundary / restore)."""
+        src = kernels.pool_source(pairs.contiguous())
+        # pool_source numbers the blocks of `pairs` from 0; shift by addressing from `first` back.
+        shifted = kernels.Source(src.k - first * src.block_stride * pairs.element_size(), src.v - first * src.block_stride * pairs.element_size(),
+                                 src.block_stride, src.head_stride, src.dtype, src.deq_dtype, first + pairs.shape[0], src.owners)
+        self._store(shifted, first, pairs.shape[0], with_store=True)
+        self.n_sealed = max(self.n_sealed, first + pairs.shape[0])
+
+    def set_current(self, keys: torch.Tensor, values: torch.Tensor, fill: int) -> None:
+        """Sink and current block: keys/values [h, 2, bs, d] slices are written by the caller via `pool`."""
+        self.fill = fill
+        self.length = self.n_sealed * self.bs + fill
+
+    def append(self, key: torch.Tensor, value: torch.Tensor, counters: TierCounters | None = None) -> None:
+        """Write one decode token; seal the current block first if it is full (lazykv/tiered.py:306-314)."""
+        if self.fill == self.bs:
+            self._seal(counters)
+        self.pool[1, :, 0, self.fill].copy_(key[0, :, 0])
+        self.pool[1, :, 1, self.fill].copy_(value[0, :, 0])
+        self.fill += 1
+        self.length += 1
+
+    def _seal(self, counters: TierCounters | None) -> None:
+        """Store the full current block as block n_sealed (lazykv/tiered.py:353-375), on the device."""
+        b = self.n_sealed
+        if b >= self.cap_blocks:
+            raise RuntimeError(f"host pool full: {self.cap_blocks} blocks")
+        # Slot 1 of the pool, addressed as block b of a source whose block stride is zero.
+        slot = self._pool_src
+        src = kernels.Source(slot.k + self.h * 2 * self.bs * self.d * self.pool.element_size(), slot.v + self.h * 2 * self.bs * self.d * self.pool.element_size(),
+                             0, slot.head_stride, slot.dtype, slot.deq_dtype, self.cap_blocks, slot.owners)
+        self._store(src, b, 1, with_store=True)
+        self.n_sealed += 1
+        self.fill = 0
+        if counters is not None:
+            counters.seals += 1
+            counters.seal_bytes += self.h * self.pair_bytes
+
+    # -- decode ---------------------------------------------------------------------------------
+
+    def candidates(self) -> tuple[int, int]:
+        """(n_full, fill): blocks 1..n_full-1 are selectable, block n_full is current (:379-381)."""
+        return self.n_sealed, self.fill
+
+    def rank(self, query: torch.Tensor, out: torch.Tensor | None = None, ws: kernels.Workspace | None = None) -> torch.Tensor:
+        """Top-K block ids [h, K] (int32, ascending, on the device) for a query [1, n_q, 1, d]."""
+        n_full, _ = self.candidates()
+        if n_full - 1 < self.k:
+            raise ValueError(f"budget of {self.k} blocks covers all {n_full - 1} candidate blocks")
+        idx = kernels.bound_topk(query, self.kmin, self.kmax, self.k, cand_offset=1, n_cand=n_full - 1, rank_mode=self.rank_mode, out_idx=out, ws=ws)
+        assert idx is not None
+        return idx
+
+    def rank_host(self, query: torch.Tensor) -> np.ndarray:
+        """The reference's `rank` (:383-387): ids [h, K] in descending bound order, on the host (syncs)."""
+        n_full, _ = self.candidates()
+        idx = kernels.bound_topk(query, self.kmin, self.kmax, self.k, cand_offset=1, n_cand=n_full - 1, rank_mode=self.rank_mode, sorted_=True)
+        return idx.to(torch.int64).cpu().numpy()
+
+    def decode(self, query: torch.Tensor, scaling: float | None, idx: torch.Tensor | None = None, out: torch.Tensor | None = None, lse: torch.Tensor | None = None, ws: kernels.Workspace | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Attention of one decode token over this layer's attended set. Returns out [n_q, d], lse [n_q]."""
+        if idx is None:
+            idx = self.rank(query, ws=ws)
+        n_full, fill = self.candidates()
+        sel = self._store_src if self.fetch == "resident" else self._host_src
+        rem = None
+        rem_range = (0, 0)
+        if self.exact:
+            rem, rem_range = self._host_src, (1, n_full)
+        scale = scaling if scaling is not None else self.d**-0.5
+        return kernels.sparse_decode(
+            query.reshape(-1, self.d), n_kv=self.h, block_size=self.bs, scale=scale, sel=sel, idx=idx,
+            sink=self._pool_src, sink_block=0, cur=self._pool_src, cur_block=1 if fill > 0 else -1, fill=fill,
+            rem=rem, rem_range=rem_range, out=out, lse=lse, ws=ws,
+        )
+
+    def gpu_bytes(self) -> int:
+        store = self.store.numel() * self.store.element_size() if self.store is not None else 0
+        return self.pool.numel() * self.pool.element_size() + store
+
+    def metadata_bytes(self) -> int:
+        return 2 * self.kmin.numel() * self.kmin.element_size()
+
+    def host_bytes(self) -> int:
+        return self.n_sealed * self.h * self.pair_bytes if self.host is not None else 0
+
+
+class TieredCache:
+    """Decode-time cache: dense layers are the caller's, selecting layers are tiered (lazykv/tiered.py:538-747).
+
+    Build it from prefilled per-layer KV (`layers`: list of (keys, values) [1, h, L, d] on the GPU)
+    or from prebuilt `tiers`. `select` returns a `Decoded` (the finished attention of the step), or
+    None to attend densely (dense layers, multi-token forwards).
+    """
+
+    def __init__(
+        self,
+        layers: list[tuple[torch.Tensor, torch.Tensor]] | None,
+        k_blocks: int,
+        block_size: int,
+        capacity_tokens: int,
+        dense_layers: int = QUEST_DENSE_LAYERS,
+        host_pools: list[torch.Tensor] | None = None,
+        n_slots: int | None = None,
+        fetch: str = "zerocopy",
+        quant: str | None = None,
+        exact: bool = False,
+        tiers: dict[int, TieredLayer] | None = None,
+        rank_dtype: torch.dtype | None = torch.float32,
+        prefetch: bool = False,
+        record_selection: bool = False,
+        replay_selection: Any = None,
+    ) -> None:
+        if fetch not in FETCH_MODES:
+            raise ValueError(f"unknown fetch mode {fetch!r}")
+        if fetch == "zerocopy" and (prefetch or record_selection or replay_selection is not None):
+            # lazykv/tiered.py:573-577: nothing to prefetch, record or replay without residency.
+            raise ValueError("the zero-copy fetch has no residency to prefetch, record or replay")
+        if prefetch or record_selection or replay_selection is not None:
+            raise ValueError("residency prefetch / record / replay are rung 6-7 features outside this path")
+        self.k_blocks, self.block_size, self.dense_layers = k_blocks, block_size, dense_layers
+        self.fetch, self.quant, self.exact = fetch, quant, exact
+        self.counters = TierCounters()
+        self.dense: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+        if tiers is None:
+            if layers is None:
+                raise ValueError("need prefilled layers or prebuilt tiers")
+            tiers = {}
+            for i in range(dense_layers, len(layers)):
+                k, v = layers[i]
+                host = None if host_pools is None else host_pools[i - dense_layers]
+                tiers[i] = TieredLayer(k, v, k_blocks, block_size, capacity_tokens, host, n_slots, quant=quant, fetch=fetch, exact=exact, rank_dtype=rank_dtype)
+            for i in range(min(dense_layers, len(layers))):
+                self.dense[i] = layers[i]
+        self.tiers = tiers
+        for t in tiers.values():
+            self.counters.boundary_d2h_bytes += t.boundary_d2h_bytes
+        first = next(iter(tiers.values()))
+        dev = first.pool.device
+        # One index buffer and one workspace shared by every layer: layers run in order on one stream.
+        self._idx = torch.empty((first.h, k_blocks), dtype=torch.int32, device=dev)
+        self._ws = kernels.Workspace(dev)
+        self.policy_name = "tiered_exact" if exact else ("tiered_int8" if quant else f"tiered_{fetch}")
+
+    # -- transformers plumbing --------------------------------------------------------------------
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, *args: object, **kwargs: object) -> tuple[torch.Tensor, torch.Tensor]:
+        tier = self.tiers.get(layer_idx)
+        if tier is None:
+            raise RuntimeError(f"layer {layer_idx} is dense; its KV belongs to the caller's cache")
+        if key_states.shape[-2] != 1:
+            raise NotImplementedError("multi-token ingestion into the tier is outside the decode path")
+        tier.append(key_states, value_states, self.counters)
+        return tier.pool[1:2, :, 0], tier.pool[1:2, :, 1]
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        tier = self.tiers.get(layer_idx)
+        if tier is not None:
+            return tier.length
+        k, _ = self.dense[layer_idx]
+        return k.shape[2]
+
+    def model_kwargs(self) -> dict[str, object]:
+        return {"lazykv_selector": self}
+
+    # -- decode path ----------------------------------------------------------------------------
+
+    def select(self, layer_idx: int, query: torch.Tensor, key: torch.Tensor | None = None, value: torch.Tensor | None = None, scaling: float | None = None) -> Decoded | None:
+        tier = self.tiers.get(layer_idx)
+        if tier is None or query.shape[-2] != 1:
+            return None
+        idx = tier.rank(query, out=self._idx, ws=self._ws)
+        out, lse = tier.decode(query, scaling, idx=idx, ws=self._ws)
+        c = self.counters
+        c.selections += 1
+        c.selected_pairs += tier.h * tier.k
+        if tier.fetch == "zerocopy":
+            c.zerocopy_bytes += tier.h * tier.k * tier.pair_bytes
+        if tier.exact:
+            c.remainder_pairs += tier.h * (tier.n_sealed - 1 - tier.k)
+        n_q = out.shape[0]
+        return Decoded(out.view(1, n_q, 1, tier.d), lse.view(1, n_q))
+
+    def close(self) -> None:
+        pass
+
+    def counters_dict(self) -> dict[str, Any]:
+        from dataclasses import asdict
+
+        return asdict(self.counters)
+
+
+class ExactTieredCache(TieredCache):
+    """Rung 9 on the GPU: selected blocks from HBM, every other sealed block from the host tier,
+    merged exactly (lazykv/exact.py:155-264). Unlike the reference, an int8 host tier is allowed:
+    the cold partial is computed from the dequantised records, inside the same kernel."""
+
+    def __init__(self, layers, k_blocks, block_size, capacity_tokens, **kwargs: Any) -> None:  # noqa: ANN001
+        if kwargs.get("prefetch"):
+            raise ValueError("rung 9 does not prefetch; the cold set is attended, not fetched")
+        kwargs["exact"] = True
+        kwargs.setdefault("fetch", "resident")
+        super().__init__(layers, k_blocks, block_size, capacity_tokens, **kwargs)
