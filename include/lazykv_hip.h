@@ -10,10 +10,9 @@
  *    PCIe in place.
  *  - `stream` is a hipStream_t passed as an integer (0 = the null stream). Work is enqueued only:
  *    no entry point synchronises the stream, and none allocates device memory. Scratch space is
- *    the caller's `ws` buffer, sized by the matching *_workspace_bytes function; it must be zeroed
- *    once before its first use and is left zeroed by every successful kernel (arrival counters
- *    reset themselves), so it can be reused across calls on one stream. Calls that overlap on
- *    different streams need distinct workspaces.
+ *    the caller's `ws` buffer, sized by the matching *_workspace_bytes function; it needs no
+ *    initialisation and can be reused by calls issued in order on one stream. Calls that overlap
+ *    on different streams need distinct workspaces.
  *  - Return value: LKV_OK (0) or a negative LKV_ERR_*; shapes and arguments are validated before
  *    any launch. lkv_last_error() returns a message for the calling thread's last failure.
  *  - Dtype codes: LKV_F16, LKV_BF16, LKV_F32 for model-dtype tensors; LKV_INT8_RECORD for the

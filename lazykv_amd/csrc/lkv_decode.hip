@@ -18,8 +18,10 @@
 // (l & 15) * D/16 ..: one 16-byte load per lane covers 4 rows. Scores are 16-lane DPP sums; the
 // online softmax runs in base 2 with the scale folded into q.
 //
-// Merge. Waves combine in LDS, workgroups write (m, l, o) partials to the workspace, and the last
-// workgroup of each head (arrival counter, self-resetting) folds them into out and lse.
+// Merge. Waves combine in LDS, workgroups write (m, l, o) partials to the workspace, and a second
+// launch folds each query head's partials into out and lse. (A last-arriver merge inside one
+// launch would need a device-scope release per workgroup, which writes back the whole L2; the
+// kernel boundary publishes every partial once.)
 #include "lkv_common.h"
 
 namespace {
@@ -53,7 +55,6 @@ struct DecodeArgs {
   void* out;
   int out_dtype;
   float* lse;
-  uint32_t* counters;
   float* part_ml;  // [n_kv][S][G][2]
   float* part_o;   // [n_kv][S][G][D]
 };
@@ -213,13 +214,8 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
   const int S = a.splits_a + a.splits_b;
 
   __shared__ float s_m[kWaves][G], s_l[kWaves][G];
-  // The wave partials (before the arrival) and the merge weights (after it) share storage.
-  constexpr int kBufWords = kWaves * D > kMaxSplits ? kWaves * D : kMaxSplits;
-  __shared__ float s_buf[G * kBufWords];
-  float(*s_o)[G][D] = reinterpret_cast<float(*)[G][D]>(s_buf);         // [kWaves][G][D]
-  float(*s_w)[kMaxSplits] = reinterpret_cast<float(*)[kMaxSplits]>(s_buf);  // [G][kMaxSplits]
+  __shared__ float s_o[kWaves][G][D];
   __shared__ uint32_t s_excl[64];  // segment B: bitmap of excluded blocks in this run
-  __shared__ uint32_t s_last;
 
   float q[G][EPL];
 #pragma unroll
@@ -310,55 +306,57 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
       pml[2 * j + 1] = L;
     }
   }
+}
 
-  // ---- arrival: the last workgroup of the head merges every partial ----------------------------
-  lkv::release_device();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = lkv::arrive(&a.counters[h]);
-    s_last = old == (uint32_t)(S - 1) ? 1u : 0u;
-    if (s_last) lkv::reset_counter(&a.counters[h]);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  lkv::acquire_device();
-
-  const float* ml_h = a.part_ml + (int64_t)h * S * G * 2;
-  const float* o_h = a.part_o + (int64_t)h * S * G * D;
-  __shared__ float s_M[G], s_L[G];
-  for (int j = wave; j < G; j += kWaves) {
-    float M = -INFINITY;
-    for (int s = lane; s < S; s += 64) M = fmaxf(M, __builtin_nontemporal_load(&ml_h[(s * G + j) * 2]));
+// Folds the S partials of one query head into its output and LSE. One workgroup per query head,
+// one thread per channel.
+template <int D, int G>
+__global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_o,
+                                                         int S, void* __restrict__ out, int out_dtype,
+                                                         float* __restrict__ lse) {
+  const int row = blockIdx.x;  // query head h * G + j
+  const int h = row / G, j = row % G;
+  const int t = threadIdx.x;
+  const float* ml = part_ml + (int64_t)h * S * G * 2;
+  const float* o = part_o + (int64_t)h * S * G * D;
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_red[D / 64 > 0 ? D / 64 : 1];
+  __shared__ float s_M, s_L;
+  float M = -INFINITY;
+  for (int s = t; s < S; s += D) M = fmaxf(M, ml[(s * G + j) * 2]);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    float L = 0.0f;
-    if (M != -INFINITY) {
-      for (int s = lane; s < S; s += 64) {
-        const float ms = __builtin_nontemporal_load(&ml_h[(s * G + j) * 2]);
-        const float w = exp2f(ms - M);
-        s_w[j][s] = w;
-        L += __builtin_nontemporal_load(&ml_h[(s * G + j) * 2 + 1]) * w;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
-    if (lane == 0) {
-      s_M[j] = M;
-      s_L[j] = L;
-    }
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  if ((t & 63) == 0) s_red[t >> 6] = M;
+  __syncthreads();
+  if (t == 0) {
+    float m = s_red[0];
+    for (int w = 1; w < D / 64; ++w) m = fmaxf(m, s_red[w]);
+    s_M = m;
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < G * D; t += kThreads) {
-    const int j = t / D;
-    const float M = s_M[j], L = s_L[j];
-    float O = 0.0f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < S; ++s) O += __builtin_nontemporal_load(&o_h[(int64_t)s * G * D + t]) * s_w[j][s];
-    }
-    const int row = h * G + j;
-    lkv::store_any(a.out, (int64_t)row * D + (t % D), a.out_dtype, L > 0.0f ? O / L : 0.0f);
-    if (t % D == 0) a.lse[row] = (M == -INFINITY || !(L > 0.0f)) ? -INFINITY : (M + log2f(L)) * lkv::kLn2;
+  M = s_M;
+  float L = 0.0f;
+  for (int s = t; s < S; s += D) {
+    const float w = M == -INFINITY ? 0.0f : exp2f(ml[(s * G + j) * 2] - M);
+    s_w[s] = w;
+    L += ml[(s * G + j) * 2 + 1] * w;
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+  __syncthreads();
+  if ((t & 63) == 0) s_red[t >> 6] = L;
+  __syncthreads();
+  if (t == 0) {
+    float l = 0.0f;
+    for (int w = 0; w < D / 64; ++w) l += s_red[w];
+    s_L = l;
+  }
+  __syncthreads();
+  L = s_L;
+  float O = 0.0f;
+  for (int s = 0; s < S; ++s) O += o[((int64_t)s * G + j) * D + t] * s_w[s];
+  lkv::store_any(out, (int64_t)row * D + t, out_dtype, L > 0.0f ? O / L : 0.0f);
+  if (t == 0) lse[row] = (M == -INFINITY || !(L > 0.0f)) ? -INFINITY : (M + log2f(L)) * lkv::kLn2;
 }
 
 struct Plan {
@@ -387,6 +385,9 @@ int launch(hipStream_t stream, DecodeArgs& a) {
   const int S = a.splits_a + a.splits_b;
   hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G>), dim3(S * a.n_kv), dim3(kThreads), 0, stream, a);
   LKV_CHECK_LAUNCH("sparse_decode");
+  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(D), 0, stream, a.part_ml, a.part_o, S, a.out,
+                     a.out_dtype, a.lse);
+  LKV_CHECK_LAUNCH("decode_merge");
   return LKV_OK;
 }
 
@@ -435,8 +436,7 @@ extern "C" size_t lkv_sparse_decode_workspace_bytes(const lkv_decode_desc* d) {
   const Plan p = make_plan(d);
   const size_t S = (size_t)(p.splits_a + p.splits_b);
   const size_t G = (size_t)(d->n_q / d->n_kv);
-  return lkv_align_up((size_t)d->n_kv * 4, 256) + lkv_align_up((size_t)d->n_kv * S * G * 2 * 4, 256) +
-         lkv_align_up((size_t)d->n_kv * S * G * d->head_dim * 4, 256);
+  return lkv_align_up((size_t)d->n_kv * S * G * 2 * 4, 256) + lkv_align_up((size_t)d->n_kv * S * G * d->head_dim * 4, 256);
 }
 
 extern "C" int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
@@ -524,8 +524,6 @@ extern "C" int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, 
   a.lse = lse;
   const int G = d.n_q / d.n_kv;
   char* w = (char*)ws;
-  a.counters = (uint32_t*)w;
-  w += lkv_align_up((size_t)d.n_kv * 4, 256);
   a.part_ml = (float*)w;
   w += lkv_align_up((size_t)d.n_kv * S * G * 2 * 4, 256);
   a.part_o = (float*)w;

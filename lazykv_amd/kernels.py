@@ -21,12 +21,11 @@ from lazykv_amd.pinned import device_address, is_mapped
 
 
 class Workspace:
-    """A zero-initialised device scratch buffer, grown on demand.
+    """A device scratch buffer (partials, bounds), grown on demand.
 
-    Kernels that use one leave it zeroed (their arrival counters reset themselves), so one
-    workspace serves any number of calls issued in order on one stream. Growing it allocates a
-    fresh zeroed buffer, so the caller must not grow it while earlier calls may still be running on
-    another stream.
+    Its contents need no initialisation, so one workspace serves any number of calls issued in
+    order on one stream. Growing it allocates a fresh buffer; calls already prepared against the
+    old one keep it alive.
     """
 
     def __init__(self, device: torch.device | str | None = None, nbytes: int = 0) -> None:
@@ -327,3 +326,66 @@ def unpack_int8(records: torch.Tensor, block_size: int, head_dim: int, dtype: to
 def stream_read(src_addr: int, nbytes: int, blocks: int, sink: torch.Tensor) -> None:
     """Launch the link probe over `nbytes` at a device-visible address; sink is uint32 [>= blocks] on the GPU."""
     _lib.check(_lib.lib().lkv_stream_read(_lib.stream_of(sink), src_addr, nbytes, blocks, sink.data_ptr()), "stream_read")
+
+
+# -- prepared launches ------------------------------------------------------------------------------
+
+
+class PreparedBoundTopk:
+    """`bound_topk` with every argument converted once; calling it only launches.
+
+    For loops that issue the same selection per step (a decode step over many layers), or for
+    capture into a HIP graph: the stream is read at call time.
+    """
+
+    def __init__(self, q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, out_idx: torch.Tensor, rank_mode: int = _lib.RANK_F32, ws: Workspace | None = None) -> None:
+        _lib.require_cuda(q, kmin, kmax, out_idx)
+        n_kv, cap, d, hs = _meta_layout(kmin, kmax)
+        if cand_offset < 1 or cand_offset + n_cand > cap or k > n_cand:
+            raise ValueError("candidate range outside the metadata, or k > n_cand")
+        if out_idx.dtype != torch.int32 or tuple(out_idx.shape) != (n_kv, k) or not out_idx.is_contiguous():
+            raise ValueError(f"out_idx must be contiguous int32 [{n_kv}, {k}]")
+        qq = q.reshape(-1, d)
+        if not qq.is_contiguous() or qq.shape[0] % n_kv:
+            raise ValueError("query must be contiguous [n_q, d] with n_q a multiple of the KV heads")
+        ws = ws or default_workspace(q.device)
+        ws_ptr, ws_n = ws.get(_lib.lib().lkv_bound_topk_workspace_bytes(n_kv, n_cand, k))
+        self._keep = (q, kmin, kmax, out_idx, ws.buf)
+        self._fn = _lib.lib().lkv_bound_topk
+        self._args = (qq.data_ptr(), _lib.dtype_code(qq.dtype), address(kmin[0] if kmin.ndim == 4 else kmin), address(kmax[0] if kmax.ndim == 4 else kmax),
+                      _lib.dtype_code(kmin.dtype), hs, qq.shape[0], n_kv, d, cand_offset, n_cand, k, rank_mode, 0, out_idx.data_ptr(), k, None, ws_ptr, ws_n)
+        self.device = q.device
+
+    def __call__(self) -> None:
+        rc = self._fn(torch.cuda.current_stream(self.device).cuda_stream, *self._args)
+        if rc:
+            _lib.check(rc, "bound_topk")
+
+
+class PreparedDecode:
+    """`sparse_decode` with every argument converted once; `desc` fields (fill, cur_block, rem
+    range) may be updated between calls without re-preparing."""
+
+    def __init__(self, q: torch.Tensor, *, n_kv: int, block_size: int, scale: float, sel: Source | None, idx: torch.Tensor | None, sink: Source | None, sink_block: int,
+                 cur: Source | None, cur_block: int, fill: int, out: torch.Tensor, lse: torch.Tensor, rem: Source | None = None, rem_range: tuple[int, int] = (0, 0),
+                 attend_selected: bool = True, ws: Workspace | None = None, max_rem_blocks: int = 0) -> None:
+        qq = q.reshape(-1, q.shape[-1])
+        n_q, d = qq.shape
+        k = idx.shape[1] if idx is not None else 0
+        self.desc = _lib.DecodeDesc(n_q, n_kv, d, block_size, float(scale), k, 1 if attend_selected else 0, sink_block, cur_block, fill, rem_range[0], rem_range[1])
+        # Size the workspace for the largest remainder this call will be updated to.
+        sizing = _lib.DecodeDesc(n_q, n_kv, d, block_size, float(scale), k, 1 if attend_selected else 0, sink_block, cur_block, fill, 0, max(rem_range[1] - rem_range[0], max_rem_blocks))
+        ws = ws or default_workspace(q.device)
+        ws_ptr, ws_n = ws.get(max(_lib.lib().lkv_sparse_decode_workspace_bytes(ctypes.byref(self.desc)), _lib.lib().lkv_sparse_decode_workspace_bytes(ctypes.byref(sizing))))
+        self._c = [s.c() if s is not None else None for s in (sel, sink, cur, rem)]
+        refs = [ctypes.byref(c) if c is not None else None for c in self._c]
+        self._keep = (q, idx, out, lse, ws.buf, sel, sink, cur, rem)
+        self._fn = _lib.lib().lkv_sparse_decode
+        self._args = (ctypes.byref(self.desc), qq.data_ptr(), _lib.dtype_code(qq.dtype), refs[0], idx.data_ptr() if idx is not None else None, k,
+                      refs[1], refs[2], refs[3], out.data_ptr(), _lib.dtype_code(out.dtype), lse.data_ptr(), ws_ptr, ws_n)
+        self.device = q.device
+
+    def __call__(self) -> None:
+        rc = self._fn(torch.cuda.current_stream(self.device).cuda_stream, *self._args)
+        if rc:
+            _lib.check(rc, "sparse_decode")
