@@ -165,6 +165,24 @@ __device__ __forceinline__ void load_row_segment(const typename Elem<DT>::T* p, 
   }
 }
 
+// Load the G query rows' segments this lane needs: q[(h*G + j) * D + c*EPL .. +EPL) for j < G,
+// widened to float. One vector load per row; the dtype switch is uniform and outside the loads,
+// so all G loads are in flight together.
+template <int D, int G, int EPL>
+__device__ __forceinline__ void load_query_rows(const void* q, int q_dtype, int h, int c, float (&out)[G][EPL]) {
+  const int64_t base = (int64_t)h * G * D + c * EPL;
+  if (q_dtype == LKV_BF16) {
+#pragma unroll
+    for (int j = 0; j < G; ++j) load_row_segment<LKV_BF16, EPL>((const uint16_t*)q + base + (int64_t)j * D, out[j]);
+  } else if (q_dtype == LKV_F16) {
+#pragma unroll
+    for (int j = 0; j < G; ++j) load_row_segment<LKV_F16, EPL>((const uint16_t*)q + base + (int64_t)j * D, out[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < G; ++j) load_row_segment<LKV_F32, EPL>((const float*)q + base + (int64_t)j * D, out[j]);
+  }
+}
+
 // ---- cross-lane reductions -------------------------------------------------------------------
 // DPP control words (GFX9): quad permutes, half-row mirror (lane i <-> 7-i within 8),
 // row mirror (lane i <-> 15-i within 16). Pairing lanes this way sums a full 16-lane row in

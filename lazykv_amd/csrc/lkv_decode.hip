@@ -22,6 +22,8 @@
 // launch folds each query head's partials into out and lse. (A last-arriver merge inside one
 // launch would need a device-scope release per workgroup, which writes back the whole L2; the
 // kernel boundary publishes every partial once.)
+#include <type_traits>
+
 #include "lkv_common.h"
 
 namespace {
@@ -59,16 +61,53 @@ struct DecodeArgs {
   float* part_o;   // [n_kv][S][G][D]
 };
 
-// One chunk of up to 16 tokens of a pair, widened to float: k[i], v[i] are rows r + 4i.
-template <int EPL>
-struct Chunk {
-  float k[4][EPL];
-  float v[4][EPL];
+// Raw register image of one chunk (up to 16 tokens) of a pair, exactly as loaded; it is widened
+// to float only when consumed, so a wave can keep two pairs' loads in flight in few registers.
+// Rows r + 4i (i < 4) of the chunk, this lane's D/16 channels.
+template <int D, int MT>
+struct RawModel {
+  static constexpr int EPL = D / 16;
+  static constexpr int W = EPL * (int)sizeof(typename lkv::Elem<MT>::T) / 4;  // words per row segment
+  uint32_t k[4][W];
+  uint32_t v[4][W];
 };
 
+// int8 record of lazykv/quant.py:46-56: kq[bs][D] | vq[bs][D] | ks[D] | kz[D] | vs[bs] | vz[bs].
+template <int D>
+struct RawI8 {
+  static constexpr int EPL = D / 16;
+  static constexpr int W = EPL / 4;  // int8 words per row segment
+  uint32_t k[4][W];
+  uint32_t v[4][W];
+  uint32_t ks[EPL / 2];  // float16 pairs of this lane's channels
+  uint32_t kz[EPL / 2];
+  uint32_t vs[4];  // float16 in the low half
+  uint32_t vz[4];
+};
+
+template <int W>
+__device__ __forceinline__ void load_words(const void* p, uint32_t (&w)[W]) {
+  if constexpr (W == 1) {
+    w[0] = *(const uint32_t*)p;
+  } else if constexpr (W == 2) {
+    const uint2 x = *(const uint2*)p;
+    w[0] = x.x;
+    w[1] = x.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const uint4 x = ((const uint4*)p)[i];
+      w[4 * i] = x.x;
+      w[4 * i + 1] = x.y;
+      w[4 * i + 2] = x.z;
+      w[4 * i + 3] = x.w;
+    }
+  }
+}
+
 template <int D, int MT>
-__device__ __forceinline__ void load_chunk_model(const Src& s, int block, int h, int t0, int nit, int limit, int r,
-                                                 int c, Chunk<D / 16>& ch) {
+__device__ __forceinline__ void load_raw(const Src& s, int block, int h, int t0, int nit, int limit, int r, int c,
+                                         RawModel<D, MT>& raw) {
   using T = typename lkv::Elem<MT>::T;
   constexpr int EPL = D / 16;
   const int64_t off = (int64_t)block * s.bstride + (int64_t)h * s.hstride + c * EPL;
@@ -78,59 +117,90 @@ __device__ __forceinline__ void load_chunk_model(const Src& s, int block, int h,
   for (int i = 0; i < 4; ++i) {
     const int row = t0 + r + 4 * i;
     if (i < nit && row < limit) {  // rows past `limit` may lie past the end of the source
-      lkv::load_row_segment<MT, EPL>(kb + (int64_t)row * D, ch.k[i]);
-      lkv::load_row_segment<MT, EPL>(vb + (int64_t)row * D, ch.v[i]);
+      load_words(kb + (int64_t)row * D, raw.k[i]);
+      load_words(vb + (int64_t)row * D, raw.v[i]);
     } else {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) ch.k[i][e] = ch.v[i][e] = 0.0f;
+      for (int w = 0; w < RawModel<D, MT>::W; ++w) raw.k[i][w] = raw.v[i][w] = 0u;
     }
   }
 }
 
-// int8 record of lazykv/quant.py:46-56: kq[bs][D] | vq[bs][D] | ks[D] | kz[D] | vs[bs] | vz[bs].
-// Dequantisation (quant.py:103-105): ((q + 128) * scale) + zero, float32 multiply and add
-// rounded separately (this file is built without FP contraction), then rounded to the model dtype.
-template <int D, int MT>
-__device__ __forceinline__ void load_chunk_i8(const Src& s, int bs, int block, int h, int t0, int nit, int limit, int r,
-                                              int c, Chunk<D / 16>& ch) {
+template <int D>
+__device__ __forceinline__ void load_raw(const Src& s, int bs, int block, int h, int t0, int nit, int limit, int r, int c,
+                                         RawI8<D>& raw) {
   constexpr int EPL = D / 16;
   const uint8_t* rec = (const uint8_t*)s.k + (int64_t)block * s.bstride + (int64_t)h * s.hstride;
   const uint16_t* scales = (const uint16_t*)(rec + 2 * bs * D);
-  float ks[EPL], kz[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    ks[e] = lkv::f16_to_f32(scales[c * EPL + e]);
-    kz[e] = lkv::f16_to_f32(scales[D + c * EPL + e]);
-  }
+  load_words(scales + c * EPL, raw.ks);
+  load_words(scales + D + c * EPL, raw.kz);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = t0 + r + 4 * i;
     if (i < nit && row < limit) {
-      const float vs = lkv::f16_to_f32(scales[2 * D + row]);
-      const float vz = lkv::f16_to_f32(scales[2 * D + bs + row]);
-      const int8_t* kq = (const int8_t*)rec + row * D + c * EPL;
-      const int8_t* vq = (const int8_t*)rec + bs * D + row * D + c * EPL;
-      int8_t kb[EPL], vb[EPL];
-      if constexpr (EPL == 8) {
-        uint2 a = *(const uint2*)kq, b = *(const uint2*)vq;
-        __builtin_memcpy(kb, &a, 8);
-        __builtin_memcpy(vb, &b, 8);
-      } else {
-        uint32_t a = *(const uint32_t*)kq, b = *(const uint32_t*)vq;
-        __builtin_memcpy(kb, &a, 4);
-        __builtin_memcpy(vb, &b, 4);
-      }
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        ch.k[i][e] = lkv::round_through<MT>(((float)kb[e] + 128.0f) * ks[e] + kz[e]);
-        ch.v[i][e] = lkv::round_through<MT>(((float)vb[e] + 128.0f) * vs + vz);
-      }
+      load_words(rec + row * D + c * EPL, raw.k[i]);
+      load_words(rec + bs * D + row * D + c * EPL, raw.v[i]);
+      raw.vs[i] = scales[2 * D + row];
+      raw.vz[i] = scales[2 * D + bs + row];
     } else {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) ch.k[i][e] = ch.v[i][e] = 0.0f;
+      for (int w = 0; w < RawI8<D>::W; ++w) raw.k[i][w] = raw.v[i][w] = 0u;
+      raw.vs[i] = raw.vz[i] = 0u;
     }
   }
 }
+
+// Per-row widening of a raw chunk: key row i / value row i of this lane's channels, as float.
+template <int D, int MT>
+struct Widen {
+  using Raw = RawModel<D, MT>;
+  static constexpr int EPL = D / 16;
+  __device__ __forceinline__ explicit Widen(const Raw&) {}
+  __device__ __forceinline__ static float elem(const uint32_t* w, int e) {
+    if constexpr (MT == LKV_F32) {
+      return lkv::bits_to_float(w[e]);
+    } else {
+      return lkv::Elem<MT>::load((uint16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu)));
+    }
+  }
+  __device__ __forceinline__ void key(const Raw& raw, int i, float (&x)[EPL]) const {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) x[e] = elem(raw.k[i], e);
+  }
+  __device__ __forceinline__ void value(const Raw& raw, int i, float (&x)[EPL]) const {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) x[e] = elem(raw.v[i], e);
+  }
+};
+
+// Dequantisation (quant.py:103-105): ((q + 128) * scale) + zero, float32 multiply and add rounded
+// separately (this file is built without FP contraction), then rounded to the model dtype.
+template <int D, int MT>
+struct WidenI8 {
+  using Raw = RawI8<D>;
+  static constexpr int EPL = D / 16;
+  float ks[EPL], kz[EPL];
+  __device__ __forceinline__ explicit WidenI8(const Raw& raw) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      ks[e] = lkv::f16_to_f32((uint16_t)((e & 1) ? (raw.ks[e >> 1] >> 16) : (raw.ks[e >> 1] & 0xffffu)));
+      kz[e] = lkv::f16_to_f32((uint16_t)((e & 1) ? (raw.kz[e >> 1] >> 16) : (raw.kz[e >> 1] & 0xffffu)));
+    }
+  }
+  __device__ __forceinline__ static float q8(const uint32_t* w, int e) {
+    return (float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xffu);
+  }
+  __device__ __forceinline__ void key(const Raw& raw, int i, float (&x)[EPL]) const {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) x[e] = lkv::round_through<MT>((q8(raw.k[i], e) + 128.0f) * ks[e] + kz[e]);
+  }
+  __device__ __forceinline__ void value(const Raw& raw, int i, float (&x)[EPL]) const {
+    const float vs = lkv::f16_to_f32((uint16_t)raw.vs[i]);
+    const float vz = lkv::f16_to_f32((uint16_t)raw.vz[i]);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) x[e] = lkv::round_through<MT>((q8(raw.v[i], e) + 128.0f) * vs + vz);
+  }
+};
 
 template <int D, int G>
 struct WaveState {
@@ -139,25 +209,30 @@ struct WaveState {
   float o[G][D / 16];
 };
 
-// Fold one chunk into the wave's running softmax. `limit`: valid tokens of this pair.
-template <int D, int G>
-__device__ __forceinline__ void consume_chunk(const float (&q)[G][D / 16], const Chunk<D / 16>& ch, int t0, int nit,
+// Fold one chunk into the wave's running softmax. `limit`: valid tokens of this pair. Rows are
+// widened one at a time from the raw registers (scores first, then the weighted values).
+template <int D, int G, typename W, typename Raw>
+__device__ __forceinline__ void consume_chunk(const float (&q)[G][D / 16], const W& wd, const Raw& raw, int t0, int nit,
                                               int limit, int r, WaveState<D, G>& st) {
   constexpr int EPL = D / 16;
   float s[4][G];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    float x[EPL];
+    wd.key(raw, i, x);
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      float a = 0.0f;
+      float acc = 0.0f;
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) a = fmaf(q[j][e], ch.k[i][e], a);
-      s[i][j] = lkv::row16_sum(a);
+      for (int e = 0; e < EPL; ++e) acc = fmaf(q[j][e], x[e], acc);
+      s[i][j] = lkv::row16_sum(acc);
     }
   }
   bool valid[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) valid[i] = i < nit && (t0 + r + 4 * i) < limit;
+  float p[4][G];
+  bool live[G];
 #pragma unroll
   for (int j = 0; j < G; ++j) {
     float cm = -INFINITY;
@@ -165,42 +240,83 @@ __device__ __forceinline__ void consume_chunk(const float (&q)[G][D / 16], const
     for (int i = 0; i < 4; ++i) cm = valid[i] ? fmaxf(cm, s[i][j]) : cm;
     cm = lkv::groups4_max(cm);
     const float m_new = fmaxf(st.m[j], cm);
-    if (m_new == -INFINITY) continue;  // nothing valid yet: state stays empty
-    const float alpha = exp2f(st.m[j] - m_new);  // exp2(-inf) = 0 on the first valid chunk
-    st.m[j] = m_new;
-    float p[4];
+    live[j] = m_new != -INFINITY;  // wave-uniform; false while nothing valid has been seen
+    const float alpha = live[j] ? exp2f(st.m[j] - m_new) : 1.0f;  // exp2(-inf) = 0 on the first valid chunk
     float psum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      p[i] = valid[i] ? exp2f(s[i][j] - m_new) : 0.0f;
-      psum += p[i];
+      p[i][j] = (valid[i] && live[j]) ? exp2f(s[i][j] - m_new) : 0.0f;
+      psum += p[i][j];
     }
-    st.l[j] = st.l[j] * alpha + psum;
+    if (live[j]) {
+      st.m[j] = m_new;
+      st.l[j] = st.l[j] * alpha + psum;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      float acc = st.o[j][e] * alpha;
+      for (int e = 0; e < EPL; ++e) st.o[j][e] *= alpha;
+    }
+  }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc = valid[i] ? fmaf(p[i], ch.v[i][e], acc) : acc;  // masked rows may hold non-finite data
-      st.o[j][e] = acc;
+  for (int i = 0; i < 4; ++i) {
+    if (!valid[i]) continue;  // masked rows may hold non-finite data
+    float x[EPL];
+    wd.value(raw, i, x);
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) st.o[j][e] = fmaf(p[i][j], x[e], st.o[j][e]);
+  }
+}
+
+// Pairs a wave keeps in flight. Measured at the 8B shape (bf16, d = 128, G = 4), one pair per
+// wave at a time (and so more waves resident) beats two for both HBM and host-memory sources.
+template <int G>
+constexpr int kPairs = 1;
+
+template <int D, int MT, typename Raw>
+__device__ __forceinline__ void load_pair_raw(const Src& s, int bs, bool ok, int block, int h, int t0, int nit,
+                                              int limit, int r, int c, Raw& raw) {
+  if (!ok) return;
+  if constexpr (std::is_same<Raw, RawI8<D>>::value) {
+    load_raw<D>(s, bs, block, h, t0, nit, limit, r, c, raw);
+  } else {
+    load_raw<D, MT>(s, block, h, t0, nit, limit, r, c, raw);
+  }
+}
+
+// Attend up to two pairs of one source: both pairs' loads are issued before either is consumed.
+// `block_b` < 0: a single pair. Ids outside the source are skipped (wave-uniform), never read.
+template <int D, int MT, int G, typename Raw>
+__device__ __forceinline__ void process_two(const DecodeArgs& a, const Src& s, int block_a, int block_b, int h,
+                                            int limit, const float (&q)[G][D / 16], int r, int c,
+                                            WaveState<D, G>& st) {
+  const bool ok_a = block_a >= 0 && (int64_t)block_a < s.nblk;
+  const bool ok_b = kPairs<G> == 2 && block_b >= 0 && (int64_t)block_b < s.nblk;
+#pragma unroll 1
+  for (int t0 = 0; t0 < a.bs; t0 += 16) {
+    const int nit = min(4, (a.bs - t0) >> 2);
+    using Wd = typename std::conditional<std::is_same<Raw, RawI8<D>>::value, WidenI8<D, MT>, Widen<D, MT>>::type;
+    Raw ra;
+    if constexpr (kPairs<G> == 2) {
+      Raw rb;
+      load_pair_raw<D, MT>(s, a.bs, ok_a, block_a, h, t0, nit, limit, r, c, ra);
+      load_pair_raw<D, MT>(s, a.bs, ok_b, block_b, h, t0, nit, limit, r, c, rb);
+      if (ok_a) consume_chunk<D, G>(q, Wd(ra), ra, t0, nit, limit, r, st);
+      if (ok_b) consume_chunk<D, G>(q, Wd(rb), rb, t0, nit, limit, r, st);
+    } else {
+      load_pair_raw<D, MT>(s, a.bs, ok_a, block_a, h, t0, nit, limit, r, c, ra);
+      if (ok_a) consume_chunk<D, G>(q, Wd(ra), ra, t0, nit, limit, r, st);
     }
   }
 }
 
 template <int D, int MT, int G>
-__device__ __forceinline__ void process_pair(const DecodeArgs& a, const Src& s, int block, int h, int limit,
-                                             const float (&q)[G][D / 16], int r, int c, WaveState<D, G>& st) {
-  if (block < 0 || (int64_t)block >= s.nblk) return;  // wave-uniform: a bad id attends nothing
-  const bool i8 = s.dtype == LKV_INT8_RECORD;
-#pragma unroll 1
-  for (int t0 = 0; t0 < a.bs; t0 += 16) {
-    const int nit = min(4, (a.bs - t0) >> 2);
-    Chunk<D / 16> ch;
-    if (i8) {
-      load_chunk_i8<D, MT>(s, a.bs, block, h, t0, nit, limit, r, c, ch);
-    } else {
-      load_chunk_model<D, MT>(s, block, h, t0, nit, limit, r, c, ch);
-    }
-    consume_chunk<D, G>(q, ch, t0, nit, limit, r, st);
+__device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, int block_a, int block_b, int h,
+                                           int limit, const float (&q)[G][D / 16], int r, int c,
+                                           WaveState<D, G>& st) {
+  if (s.dtype == LKV_INT8_RECORD) {
+    process_two<D, MT, G, RawI8<D>>(a, s, block_a, block_b, h, limit, q, r, c, st);
+  } else {
+    process_two<D, MT, G, RawModel<D, MT>>(a, s, block_a, block_b, h, limit, q, r, c, st);
   }
 }
 
@@ -218,11 +334,11 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
   __shared__ uint32_t s_excl[64];  // segment B: bitmap of excluded blocks in this run
 
   float q[G][EPL];
+  lkv::load_query_rows<D, G, EPL>(a.q, a.q_dtype, h, c, q);
 #pragma unroll
   for (int j = 0; j < G; ++j)
 #pragma unroll
-    for (int e = 0; e < EPL; ++e)
-      q[j][e] = lkv::load_any(a.q, (int64_t)(h * G + j) * D + c * EPL + e, a.q_dtype) * a.qscale;
+    for (int e = 0; e < EPL; ++e) q[j][e] *= a.qscale;
 
   WaveState<D, G> st;
 #pragma unroll
@@ -234,20 +350,22 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
   }
 
   if (split < a.splits_a) {
-    // Segment A: sink, selected, current.
+    // Segment A: sink (item 0), selected (items has_sink .. has_sink + n_sel), current (last item).
     const int first = split * a.per_a;
     const int last = min(a.n_a, first + a.per_a);
     const int has_sink = a.sink_block >= 0;
     const int n_sel = a.attend_selected ? a.k : 0;
-    for (int t = first + wave; t < last; t += kWaves) {
-      if (has_sink && t == 0) {
-        process_pair<D, MT, G>(a, a.sink, a.sink_block, h, a.bs, q, r, c, st);
-      } else if (t - has_sink < n_sel) {
-        const int b = a.idx[(int64_t)h * a.idx_stride + (t - has_sink)];
-        process_pair<D, MT, G>(a, a.sel, b, h, a.bs, q, r, c, st);
-      } else {
-        process_pair<D, MT, G>(a, a.cur, a.cur_block, h, a.fill, q, r, c, st);
-      }
+    if (has_sink && first == 0 && wave == 0) attend_two<D, MT, G>(a, a.sink, a.sink_block, -1, h, a.bs, q, r, c, st);
+    if (a.cur_block >= 0 && last == a.n_a && wave == kWaves - 1)
+      attend_two<D, MT, G>(a, a.cur, a.cur_block, -1, h, a.fill, q, r, c, st);
+    // Selected items of this run: idx positions [js, je), two per wave per round.
+    const int js = max(first, has_sink) - has_sink;
+    const int je = min(last, has_sink + n_sel) - has_sink;
+    const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
+    for (int j = js + wave; j < je; j += kPairs<G> * kWaves) {
+      const int b0 = idx_h[j];
+      const int b1 = (kPairs<G> == 2 && j + kWaves < je) ? idx_h[j + kWaves] : -1;
+      attend_two<D, MT, G>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
     }
   } else {
     // Segment B: remainder blocks of this run that idx does not name.
@@ -257,14 +375,25 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
     for (int i = threadIdx.x; i < 64; i += kThreads) s_excl[i] = 0;
     __syncthreads();
     const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
-    for (int i = threadIdx.x; i < a.k; i += kThreads) {
-      const int b = idx_h[i];
-      if (b >= lo && b < hi) atomicOr(&s_excl[(b - lo) >> 5], 1u << ((b - lo) & 31));
+    // Eight index loads in flight per thread per round.
+    for (int i0 = threadIdx.x; i0 < a.k; i0 += 8 * kThreads) {
+      int bv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) bv[u] = i0 + u * kThreads < a.k ? idx_h[i0 + u * kThreads] : -1;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (bv[u] >= lo && bv[u] < hi) atomicOr(&s_excl[(bv[u] - lo) >> 5], 1u << ((bv[u] - lo) & 31));
     }
     __syncthreads();
-    for (int b = lo + wave; b < hi; b += kWaves) {
-      if ((s_excl[(b - lo) >> 5] >> ((b - lo) & 31)) & 1u) continue;
-      process_pair<D, MT, G>(a, a.rem, b, h, a.bs, q, r, c, st);
+    int b = lo + wave;
+    while (b < hi) {
+      int pick[2] = {-1, -1};
+      int have = 0;
+      while (have < kPairs<G> && b < hi) {
+        if (!((s_excl[(b - lo) >> 5] >> ((b - lo) & 31)) & 1u)) pick[have++] = b;
+        b += kWaves;
+      }
+      if (have) attend_two<D, MT, G>(a, a.rem, pick[0], pick[1], h, a.bs, q, r, c, st);
     }
   }
 
@@ -308,55 +437,80 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
   }
 }
 
-// Folds the S partials of one query head into its output and LSE. One workgroup per query head,
-// one thread per channel.
+// Folds the S partials of one query head into its output and LSE. One workgroup of 4 waves per
+// query head: every thread loads its share of the (m, l) pairs and of the partial outputs in one
+// round of independent loads (channel t % D, partials s = t / D, t / D + 4, ...), so the merge
+// costs a few memory round trips rather than one per partial.
 template <int D, int G>
-__global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_o,
-                                                         int S, void* __restrict__ out, int out_dtype,
-                                                         float* __restrict__ lse) {
+__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_o,
+                                                           int S, void* __restrict__ out, int out_dtype,
+                                                           float* __restrict__ lse) {
+  constexpr int kT = 256;
+  constexpr int kLanesPerS = D;            // threads sharing one partial row
+  constexpr int kRowsPerRound = kT / D;    // partials read per round by the workgroup
   const int row = blockIdx.x;  // query head h * G + j
   const int h = row / G, j = row % G;
   const int t = threadIdx.x;
   const float* ml = part_ml + (int64_t)h * S * G * 2;
   const float* o = part_o + (int64_t)h * S * G * D;
   __shared__ float s_w[kMaxSplits];
-  __shared__ float s_red[D / 64 > 0 ? D / 64 : 1];
-  __shared__ float s_M, s_L;
-  float M = -INFINITY;
-  for (int s = t; s < S; s += D) M = fmaxf(M, ml[(s * G + j) * 2]);
+  __shared__ float s_red[kT / 64];
+  __shared__ float s_acc[kRowsPerRound][D];
+
+  // (m, l) of every partial: S <= kMaxSplits = 2 * kT, so two loads per thread at most.
+  float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
+  if (t < S) {
+    m0 = ml[(t * G + j) * 2];
+    l0 = ml[(t * G + j) * 2 + 1];
+  }
+  if (t + kT < S) {
+    m1 = ml[((t + kT) * G + j) * 2];
+    l1 = ml[((t + kT) * G + j) * 2 + 1];
+  }
+  float M = fmaxf(m0, m1);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
   if ((t & 63) == 0) s_red[t >> 6] = M;
   __syncthreads();
-  if (t == 0) {
-    float m = s_red[0];
-    for (int w = 1; w < D / 64; ++w) m = fmaxf(m, s_red[w]);
-    s_M = m;
-  }
+  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   __syncthreads();
-  M = s_M;
-  float L = 0.0f;
-  for (int s = t; s < S; s += D) {
-    const float w = M == -INFINITY ? 0.0f : exp2f(ml[(s * G + j) * 2] - M);
-    s_w[s] = w;
-    L += ml[(s * G + j) * 2 + 1] * w;
-  }
+  const bool any = M != -INFINITY;
+  const float w0 = (t < S && any) ? exp2f(m0 - M) : 0.0f;
+  const float w1 = (t + kT < S && any) ? exp2f(m1 - M) : 0.0f;
+  if (t < S) s_w[t] = w0;
+  if (t + kT < S) s_w[t + kT] = w1;
+  float L = l0 * w0 + l1 * w1;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
-  __syncthreads();
   if ((t & 63) == 0) s_red[t >> 6] = L;
   __syncthreads();
-  if (t == 0) {
-    float l = 0.0f;
-    for (int w = 0; w < D / 64; ++w) l += s_red[w];
-    s_L = l;
+  L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+
+  // Weighted sum of the partial outputs: thread (slice, d) takes partials slice, slice + R, ...
+  const int d = t % kLanesPerS, slice = t / kLanesPerS;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s0 = slice; s0 < S; s0 += 8 * kRowsPerRound) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + u * kRowsPerRound;
+      v[u] = s < S ? o[((int64_t)s * G + j) * D + d] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + u * kRowsPerRound;
+      acc[u] += s < S ? v[u] * s_w[s] : 0.0f;
+    }
   }
+  s_acc[slice][d] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  L = s_L;
-  float O = 0.0f;
-  for (int s = 0; s < S; ++s) O += o[((int64_t)s * G + j) * D + t] * s_w[s];
-  lkv::store_any(out, (int64_t)row * D + t, out_dtype, L > 0.0f ? O / L : 0.0f);
-  if (t == 0) lse[row] = (M == -INFINITY || !(L > 0.0f)) ? -INFINITY : (M + log2f(L)) * lkv::kLn2;
+  if (t < D) {
+    float O = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kRowsPerRound; ++q) O += s_acc[q][t];
+    lkv::store_any(out, (int64_t)row * D + t, out_dtype, L > 0.0f ? O / L : 0.0f);
+    if (t == 0) lse[row] = (!any || !(L > 0.0f)) ? -INFINITY : (M + log2f(L)) * lkv::kLn2;
+  }
 }
 
 struct Plan {
@@ -385,8 +539,8 @@ int launch(hipStream_t stream, DecodeArgs& a) {
   const int S = a.splits_a + a.splits_b;
   hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G>), dim3(S * a.n_kv), dim3(kThreads), 0, stream, a);
   LKV_CHECK_LAUNCH("sparse_decode");
-  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(D), 0, stream, a.part_ml, a.part_o, S, a.out,
-                     a.out_dtype, a.lse);
+  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(256), 0, stream, a.part_ml, a.part_o, S,
+                     a.out, a.out_dtype, a.lse);
   LKV_CHECK_LAUNCH("decode_merge");
   return LKV_OK;
 }

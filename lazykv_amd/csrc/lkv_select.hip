@@ -15,8 +15,9 @@
 // select_kernel: one 1024-thread workgroup per KV head. The bounds are mapped to order-preserving
 // integer keys in LDS and the K-th largest is found by range-adaptive radix select: each pass
 // histograms the keys of the current range into at most 2048 bins scaled to that range (so the
-// first pass spreads the clustered bounds instead of piling them into a few exponent bins), keeps
-// the bin holding the K-th key, and narrows until the range is one key. An ordered compaction
+// first pass spreads the clustered bounds instead of piling them into a few exponent bins) and
+// keeps the bin holding the K-th key; once that bin holds at most 1024 keys they are ranked
+// directly, one thread each, instead of further passes over every key. An ordered compaction
 // then writes the ids in ascending order, or a bitonic sort puts them in descending bound order
 // with ties broken towards the lower id. Scoring and selection are separate launches so that no
 // workgroup has to publish its bounds across XCDs inside one launch (a device-scope release
@@ -55,11 +56,12 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
   const int r = lane >> 4, c = lane & 15;
 
   float qp[G][EPL], qn[G][EPL];
+  lkv::load_query_rows<D, G, EPL>(q, q_dtype, h, c, qp);
 #pragma unroll
   for (int j = 0; j < G; ++j) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      float x = lkv::load_any(q, (int64_t)(h * G + j) * D + c * EPL + e, q_dtype);
+      const float x = qp[j][e];
       qp[j][e] = fmaxf(x, 0.0f);
       qn[j][e] = x - qp[j][e];
     }
@@ -159,19 +161,38 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
   uint32_t* scan = hist + kBins;
   const float* bound_h = bounds + (int64_t)h * n;
   uint32_t lmin = 0xffffffffu, lmax = 0u;
-  for (int i = threadIdx.x; i < n; i += kSelThreads) {
-    const uint32_t key = orderable(bound_h[i]);
-    keys[i] = key;
-    lmin = min(lmin, key);
-    lmax = max(lmax, key);
+  {
+    // Every load of this thread is issued before any is used (one memory round trip).
+    constexpr int kPer = kMaxCand / kSelThreads;
+    float v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = threadIdx.x + u * kSelThreads;
+      v[u] = i < n ? bound_h[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = threadIdx.x + u * kSelThreads;
+      if (i < n) {
+        const uint32_t key = orderable(v[u]);
+        keys[i] = key;
+        lmin = min(lmin, key);
+        lmax = max(lmax, key);
+      }
+    }
   }
   uint32_t lo = block_reduce_minmax(lmin, false, scan);
   uint32_t hi = block_reduce_minmax(lmax, true, scan);
 
   // ---- range-adaptive radix select of the k-th largest key --------------------------------------
   int need = k;  // keys still to take from [lo, hi]; every key above hi is taken
+  uint32_t T;    // after the loop: take every key > T and `need` keys == T
 #pragma unroll 1
-  while (lo < hi) {
+  while (true) {
+    if (lo >= hi) {
+      T = lo;
+      break;
+    }
     const uint32_t width = hi - lo;
     const int bits = 32 - __clz(width);  // width < 2^bits
     const int shift = bits > 11 ? bits - 11 : 0;
@@ -201,6 +222,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
         if ((uint32_t)need <= acc + cnt) {
           scan[kSelWaves] = (uint32_t)bin;
           scan[kSelWaves + 1] = acc;
+          scan[kSelWaves + 2] = cnt;
           break;
         }
         acc += cnt;
@@ -209,13 +231,45 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
     __syncthreads();
     const uint32_t bin = scan[kSelWaves];
     need -= (int)scan[kSelWaves + 1];
+    const uint32_t in_bin = scan[kSelWaves + 2];
     const uint32_t new_lo = lo + (bin << shift);
     const uint32_t span = shift ? ((1u << shift) - 1u) : 0u;
     hi = min(hi, new_lo + span);
     lo = new_lo;
     __syncthreads();
+    if (lo < hi && in_bin <= (uint32_t)kSelThreads) {
+      // Few keys left in the bin: rank them directly instead of more passes over all n keys.
+      // Members are listed (in any order), each ranked by (key desc, id asc); the `need` best are
+      // marked taken by raising their key above the range, the rest by dropping it below.
+      uint32_t* list_key = hist;
+      uint32_t* list_id = hist + kSelThreads;
+      if (threadIdx.x == 0) scan[kSelWaves + 3] = 0;
+      __syncthreads();
+      for (int i = threadIdx.x; i < n; i += kSelThreads) {
+        const uint32_t key = keys[i];
+        if (key >= lo && key <= hi) {
+          const uint32_t slot = atomicAdd(&scan[kSelWaves + 3], 1u);
+          list_key[slot] = key;
+          list_id[slot] = (uint32_t)i;
+        }
+      }
+      __syncthreads();
+      const int m = (int)scan[kSelWaves + 3];
+      if ((int)threadIdx.x < m) {
+        const uint32_t mk = list_key[threadIdx.x], mi = list_id[threadIdx.x];
+        int rank = 0;
+        for (int u = 0; u < m; ++u) {
+          const uint32_t uk = list_key[u];
+          rank += uk > mk || (uk == mk && list_id[u] < mi);
+        }
+        keys[mi] = rank < need ? 0xffffffffu : 0u;
+      }
+      __syncthreads();
+      T = hi;
+      need = 0;
+      break;
+    }
   }
-  const uint32_t T = lo;  // the k-th largest key; take `need` of the keys equal to it
 
   // ---- ordered compaction: ascending block id ----------------------------------------------------
   const int chunk = (n + kSelThreads - 1) / kSelThreads;
@@ -241,7 +295,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
     if (take) {
       if (pos < (uint32_t)k) {  // exactly k are taken; the guard keeps a logic error in bounds
         if (sorted) {
-          sortbuf[pos] = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+          // keys[] may hold a taken marker: sort on the bound itself.
+          sortbuf[pos] = ((uint64_t)orderable(bound_h[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
         } else {
           out_h[pos] = i + cand_offset;
         }
