@@ -437,77 +437,81 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
   }
 }
 
-// Folds the S partials of one query head into its output and LSE. One workgroup of 4 waves per
-// query head: every thread loads its share of the (m, l) pairs and of the partial outputs in one
-// round of independent loads (channel t % D, partials s = t / D, t / D + 4, ...), so the merge
-// costs a few memory round trips rather than one per partial.
+// Folds the S partials of one query head into its output and LSE. One 512-thread workgroup per
+// query head; thread t owns channel t % D of partial rows t / D, t / D + 512 / D, ... Every load
+// of a round (the partial outputs and the (m, l) pairs) is issued before any is used, so for
+// S <= 16 * 512 / D partials the merge is one memory round trip.
 template <int D, int G>
-__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_o,
+__global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_o,
                                                            int S, void* __restrict__ out, int out_dtype,
                                                            float* __restrict__ lse) {
-  constexpr int kT = 256;
-  constexpr int kLanesPerS = D;            // threads sharing one partial row
-  constexpr int kRowsPerRound = kT / D;    // partials read per round by the workgroup
-  const int row = blockIdx.x;  // query head h * G + j
+  constexpr int kT = 512;
+  constexpr int kSlices = kT / D;  // partial rows read side by side
+  constexpr int kU = 16;           // partial rows per thread per round
+  const int row = blockIdx.x;      // query head h * G + j
   const int h = row / G, j = row % G;
   const int t = threadIdx.x;
+  const int d = t % D, slice = t / D;
   const float* ml = part_ml + (int64_t)h * S * G * 2;
   const float* o = part_o + (int64_t)h * S * G * D;
   __shared__ float s_w[kMaxSplits];
   __shared__ float s_red[kT / 64];
-  __shared__ float s_acc[kRowsPerRound][D];
+  __shared__ float s_acc[kSlices][D];
 
-  // (m, l) of every partial: S <= kMaxSplits = 2 * kT, so two loads per thread at most.
-  float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
-  if (t < S) {
-    m0 = ml[(t * G + j) * 2];
-    l0 = ml[(t * G + j) * 2 + 1];
+  // First round of partial outputs, and the (m, l) pairs (S <= kMaxSplits = kT).
+  float v[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int s = slice + u * kSlices;
+    v[u] = s < S ? o[((int64_t)s * G + j) * D + d] : 0.0f;
   }
-  if (t + kT < S) {
-    m1 = ml[((t + kT) * G + j) * 2];
-    l1 = ml[((t + kT) * G + j) * 2 + 1];
-  }
-  float M = fmaxf(m0, m1);
+  const float m_t = t < S ? ml[(t * G + j) * 2] : -INFINITY;
+  const float l_t = t < S ? ml[(t * G + j) * 2 + 1] : 0.0f;
+  float M = m_t;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
   if ((t & 63) == 0) s_red[t >> 6] = M;
   __syncthreads();
-  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  M = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kT / 64; ++w) M = fmaxf(M, s_red[w]);
   __syncthreads();
   const bool any = M != -INFINITY;
-  const float w0 = (t < S && any) ? exp2f(m0 - M) : 0.0f;
-  const float w1 = (t + kT < S && any) ? exp2f(m1 - M) : 0.0f;
-  if (t < S) s_w[t] = w0;
-  if (t + kT < S) s_w[t + kT] = w1;
-  float L = l0 * w0 + l1 * w1;
+  const float w_t = (t < S && any) ? exp2f(m_t - M) : 0.0f;
+  if (t < S) s_w[t] = w_t;
+  float L = l_t * w_t;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
   if ((t & 63) == 0) s_red[t >> 6] = L;
   __syncthreads();
-  L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-
-  // Weighted sum of the partial outputs: thread (slice, d) takes partials slice, slice + R, ...
-  const int d = t % kLanesPerS, slice = t / kLanesPerS;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s0 = slice; s0 < S; s0 += 8 * kRowsPerRound) {
-    float v[8];
+  L = 0.0f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = s0 + u * kRowsPerRound;
+  for (int w = 0; w < kT / 64; ++w) L += s_red[w];
+
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int s = slice + u * kSlices;
+    if (s < S) acc += v[u] * s_w[s];
+  }
+  for (int s0 = slice + kU * kSlices; s0 < S; s0 += kU * kSlices) {  // more than kU rounds' worth
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int s = s0 + u * kSlices;
       v[u] = s < S ? o[((int64_t)s * G + j) * D + d] : 0.0f;
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = s0 + u * kRowsPerRound;
-      acc[u] += s < S ? v[u] * s_w[s] : 0.0f;
+    for (int u = 0; u < kU; ++u) {
+      const int s = s0 + u * kSlices;
+      if (s < S) acc += v[u] * s_w[s];
     }
   }
-  s_acc[slice][d] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  s_acc[slice][d] = acc;
   __syncthreads();
   if (t < D) {
     float O = 0.0f;
 #pragma unroll
-    for (int q = 0; q < kRowsPerRound; ++q) O += s_acc[q][t];
+    for (int q = 0; q < kSlices; ++q) O += s_acc[q][t];
     lkv::store_any(out, (int64_t)row * D + t, out_dtype, L > 0.0f ? O / L : 0.0f);
     if (t == 0) lse[row] = (!any || !(L > 0.0f)) ? -INFINITY : (M + log2f(L)) * lkv::kLn2;
   }
@@ -523,8 +527,10 @@ struct Plan {
 static Plan make_plan(const lkv_decode_desc* d) {
   Plan p;
   p.n_a = (d->sink_block >= 0 ? 1 : 0) + (d->attend_selected ? d->k : 0) + (d->cur_block >= 0 ? 1 : 0);
-  p.per_a = 8;
-  while (p.n_a > 0 && (p.n_a + p.per_a - 1) / p.per_a > kMaxSplits / 2) p.per_a *= 2;
+  // At least 8 items (two pairs per wave), and at most 64 partials per head so that the merge
+  // reads them in one round.
+  p.per_a = (p.n_a + 63) / 64;
+  if (p.per_a < 8) p.per_a = 8;
   p.splits_a = p.n_a > 0 ? (p.n_a + p.per_a - 1) / p.per_a : 0;
   const int n_b = d->rem_last - d->rem_first;
   p.per_b = 32;
@@ -539,7 +545,7 @@ int launch(hipStream_t stream, DecodeArgs& a) {
   const int S = a.splits_a + a.splits_b;
   hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G>), dim3(S * a.n_kv), dim3(kThreads), 0, stream, a);
   LKV_CHECK_LAUNCH("sparse_decode");
-  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(256), 0, stream, a.part_ml, a.part_o, S,
+  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(512), 0, stream, a.part_ml, a.part_o, S,
                      a.out, a.out_dtype, a.lse);
   LKV_CHECK_LAUNCH("decode_merge");
   return LKV_OK;

@@ -12,8 +12,9 @@
 // its channels of the G query heads in registers. The row sum is a 4-step DPP reduction; the max
 // over the group is taken in registers. The float32 bounds go to a scratch row per head.
 //
-// select_kernel: one 1024-thread workgroup per KV head. The bounds are mapped to order-preserving
-// integer keys in LDS and the K-th largest is found by range-adaptive radix select: each pass
+// select_kernel: one 512-thread workgroup per KV head; each thread holds a contiguous run of up to
+// 24 candidates as order-preserving integer keys in registers. The K-th largest is found by
+// range-adaptive radix select: each pass
 // histograms the keys of the current range into at most 2048 bins scaled to that range (so the
 // first pass spreads the clustered bounds instead of piling them into a few exponent bins) and
 // keeps the bin holding the K-th key; once that bin holds at most 1024 keys they are ranked
@@ -26,15 +27,22 @@
 
 namespace {
 
-constexpr int kBoundThreads = 256;
+#ifndef LKV_BOUND_THREADS
+#define LKV_BOUND_THREADS 512
+#endif
+#ifndef LKV_BOUND_ITER
+#define LKV_BOUND_ITER 1
+#endif
+constexpr int kBoundThreads = LKV_BOUND_THREADS;
 constexpr int kBoundWaves = kBoundThreads / 64;
-constexpr int kIter = 4;                                  // 4-block rows per wave per round
-constexpr int kBlocksPerWG = kBoundWaves * 4 * kIter;     // 64 candidate blocks per workgroup
-constexpr int kSelThreads = 1024;
+constexpr int kIter = LKV_BOUND_ITER;                     // 4-block rows per wave
+constexpr int kBlocksPerWG = kBoundWaves * 4 * kIter;     // candidate blocks per workgroup
+constexpr int kSelThreads = 512;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kBins = 2048;
 constexpr int kScanWords = 64;
-constexpr int kMaxCand = 12288;                           // candidates held in LDS for the select
+constexpr int kPerThread = 24;                            // candidate keys held per thread
+constexpr int kMaxCand = kSelThreads * kPerThread;        // 12288 candidates per KV head
 constexpr int kMaxSortedK = 2048;
 
 __device__ __forceinline__ uint32_t orderable(float f) {
@@ -47,7 +55,8 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
                                                               const typename lkv::Elem<MT>::T* __restrict__ kmin,
                                                               const typename lkv::Elem<MT>::T* __restrict__ kmax,
                                                               int64_t meta_head_stride, int n_kv, int cand_offset,
-                                                              int n_cand, int rank_mode, float* __restrict__ bounds) {
+                                                              int n_cand, int rank_mode, float* __restrict__ bounds,
+                                                              int64_t bound_stride) {
   using E = lkv::Elem<MT>;
   constexpr int EPL = D / 16;
   const int h = blockIdx.x % n_kv;
@@ -55,13 +64,17 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane >> 4, c = lane & 15;
 
+  // The head's G query rows are read once per workgroup into LDS: every workgroup of a head reads
+  // the same rows, and per-wave reads of them were a hot spot on a few L2 lines.
+  __shared__ float s_q[G * D];
+  for (int i = threadIdx.x; i < G * D; i += kBoundThreads) s_q[i] = lkv::load_any(q, (int64_t)h * G * D + i, q_dtype);
+  __syncthreads();
   float qp[G][EPL], qn[G][EPL];
-  lkv::load_query_rows<D, G, EPL>(q, q_dtype, h, c, qp);
 #pragma unroll
   for (int j = 0; j < G; ++j) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      const float x = qp[j][e];
+      const float x = s_q[j * D + c * EPL + e];
       qp[j][e] = fmaxf(x, 0.0f);
       qn[j][e] = x - qp[j][e];
     }
@@ -70,7 +83,7 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
   const int wg_end = min(n_cand, wg_begin + kBlocksPerWG);
   const typename E::T* kmin_h = kmin + (int64_t)h * meta_head_stride + (int64_t)cand_offset * D + c * EPL;
   const typename E::T* kmax_h = kmax + (int64_t)h * meta_head_stride + (int64_t)cand_offset * D + c * EPL;
-  float* bound_h = bounds + (int64_t)h * n_cand;
+  float* bound_h = bounds + (int64_t)h * bound_stride;
 
   float vmax[kIter][EPL], vmin[kIter][EPL];
 #pragma unroll
@@ -134,59 +147,78 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s
   return before + x - v;
 }
 
-__device__ __forceinline__ uint32_t block_reduce_minmax(uint32_t v, bool want_max, uint32_t* scan) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t y = __shfl_xor(v, o, 64);
-    v = want_max ? max(v, y) : min(v, y);
-  }
-  if (lane == 0) scan[wave] = v;
-  __syncthreads();
-  uint32_t r = scan[0];
-#pragma unroll
-  for (int w = 1; w < kSelWaves; ++w) r = want_max ? max(r, scan[w]) : min(r, scan[w]);
-  __syncthreads();
-  return r;
-}
-
-__global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __restrict__ bounds, int n_cand, int k,
-                                                             int cand_offset, int sorted, int32_t* __restrict__ out_idx,
-                                                             int64_t idx_stride) {
-  extern __shared__ uint32_t lds[];
+__global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __restrict__ bounds, int64_t bstride,
+                                                             int n_cand, int k, int cand_offset, int sorted,
+                                                             int32_t* __restrict__ out_idx, int64_t idx_stride) {
+  // Region reused in turn: histogram (kBins), then the boundary-bin list (2 * kSelThreads) and its
+  // taken bitmap, then the 64-bit sort slots (2 * kp2 <= 2 * kMaxSortedK words).
+  constexpr int kRegion = 2 * kMaxSortedK > kBins ? 2 * kMaxSortedK : kBins;
+  static_assert(2 * kSelThreads + (kMaxCand + 31) / 32 <= kRegion, "list and bitmap must fit the region");
+  __shared__ __align__(16) uint32_t region[kRegion];
+  __shared__ uint32_t scan[kScanWords];
   const int h = blockIdx.x;
   const int n = n_cand;
-  uint32_t* keys = lds;
-  uint32_t* hist = lds + ((n + 3) & ~3);  // 16-byte aligned: reused as 64-bit sort slots
-  uint32_t* scan = hist + kBins;
-  const float* bound_h = bounds + (int64_t)h * n;
-  uint32_t lmin = 0xffffffffu, lmax = 0u;
-  {
-    // Every load of this thread is issued before any is used (one memory round trip).
-    constexpr int kPer = kMaxCand / kSelThreads;
-    float v[kPer];
+  // Keys per thread, a multiple of 4 so a thread's run is whole 16-byte vectors when rows are
+  // padded (bstride % 4 == 0).
+  const int npt = ((n + kSelThreads - 1) / kSelThreads + 3) & ~3;
+  const int i0 = threadIdx.x * npt;
+  const float* bound_h = bounds + (int64_t)h * bstride;
+
+  // Each thread holds the keys of indices [i0, i0 + npt) in registers; all loads in one round.
+  uint32_t key[kPerThread];
+  if ((bstride & 3) == 0) {
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int i = threadIdx.x + u * kSelThreads;
-      v[u] = i < n ? bound_h[i] : 0.0f;
+    for (int u = 0; u < kPerThread; u += 4) {
+      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (u < npt && i0 + u < n) f = *(const float4*)(bound_h + i0 + u);  // padded row: in bounds
+      key[u] = orderable(f.x);
+      key[u + 1] = orderable(f.y);
+      key[u + 2] = orderable(f.z);
+      key[u + 3] = orderable(f.w);
     }
+  } else {
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int i = threadIdx.x + u * kSelThreads;
-      if (i < n) {
-        const uint32_t key = orderable(v[u]);
-        keys[i] = key;
-        lmin = min(lmin, key);
-        lmax = max(lmax, key);
-      }
+    for (int u = 0; u < kPerThread; ++u) key[u] = (u < npt && i0 + u < n) ? orderable(bound_h[i0 + u]) : 0u;
+  }
+  bool live[kPerThread];
+  uint32_t lmin = 0xffffffffu, lmax = 0u;
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    live[u] = u < npt && i0 + u < n;
+    if (live[u]) {
+      lmin = min(lmin, key[u]);
+      lmax = max(lmax, key[u]);
     }
   }
-  uint32_t lo = block_reduce_minmax(lmin, false, scan);
-  uint32_t hi = block_reduce_minmax(lmax, true, scan);
+  // Workgroup min and max in one reduction.
+  {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      lmin = min(lmin, (uint32_t)__shfl_xor(lmin, o, 64));
+      lmax = max(lmax, (uint32_t)__shfl_xor(lmax, o, 64));
+    }
+    if (lane == 0) {
+      scan[2 * wave] = lmin;
+      scan[2 * wave + 1] = lmax;
+    }
+    __syncthreads();
+    lmin = scan[0];
+    lmax = scan[1];
+#pragma unroll
+    for (int w = 1; w < kSelWaves; ++w) {
+      lmin = min(lmin, scan[2 * w]);
+      lmax = max(lmax, scan[2 * w + 1]);
+    }
+    __syncthreads();
+  }
+  uint32_t lo = lmin, hi = lmax;
 
   // ---- range-adaptive radix select of the k-th largest key --------------------------------------
   int need = k;  // keys still to take from [lo, hi]; every key above hi is taken
-  uint32_t T;    // after the loop: take every key > T and `need` keys == T
+  uint32_t T;    // after the loop: take every key > T, `need` keys == T, and the marked keys
+  uint32_t marked = 0u;  // bit u: key[u] lies in the final bin and ranks among the `need` best
+  uint32_t* hist = region;
 #pragma unroll 1
   while (true) {
     if (lo >= hi) {
@@ -199,9 +231,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
     const int nb = (int)(width >> shift) + 1;  // at most 2048 bins
     for (int i = threadIdx.x; i < nb; i += kSelThreads) hist[i] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += kSelThreads) {
-      const uint32_t key = keys[i];
-      if (key >= lo && key <= hi) atomicAdd(&hist[(key - lo) >> shift], 1u);
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) {
+      if (live[u] && key[u] >= lo && key[u] <= hi) atomicAdd(&hist[(key[u] - lo) >> shift], 1u);
     }
     __syncthreads();
     // Thread t owns bins [t*per, (t+1)*per); the bins above it hold `above` keys.
@@ -238,70 +270,89 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
     lo = new_lo;
     __syncthreads();
     if (lo < hi && in_bin <= (uint32_t)kSelThreads) {
-      // Few keys left in the bin: rank them directly instead of more passes over all n keys.
-      // Members are listed (in any order), each ranked by (key desc, id asc); the `need` best are
-      // marked taken by raising their key above the range, the rest by dropping it below.
-      uint32_t* list_key = hist;
-      uint32_t* list_id = hist + kSelThreads;
+      // Few keys left in the bin: rank them directly instead of more passes. They are listed (in
+      // any order) and ranked by (key desc, id asc); the `need` best are marked in a bitmap that
+      // each thread reads back for its own run of candidates.
+      uint32_t* list_key = region;
+      uint32_t* list_id = region + kSelThreads;
       if (threadIdx.x == 0) scan[kSelWaves + 3] = 0;
       __syncthreads();
-      for (int i = threadIdx.x; i < n; i += kSelThreads) {
-        const uint32_t key = keys[i];
-        if (key >= lo && key <= hi) {
+#pragma unroll
+      for (int u = 0; u < kPerThread; ++u) {
+        if (live[u] && key[u] >= lo && key[u] <= hi) {
           const uint32_t slot = atomicAdd(&scan[kSelWaves + 3], 1u);
-          list_key[slot] = key;
-          list_id[slot] = (uint32_t)i;
+          list_key[slot] = key[u];
+          list_id[slot] = (uint32_t)(i0 + u);
         }
       }
       __syncthreads();
       const int m = (int)scan[kSelWaves + 3];
+      // Thread e ranks list entry e and marks it, by index, when it is among the `need` best.
+      uint32_t* taken = region + 2 * kSelThreads;  // one bit per candidate
+      for (int i = threadIdx.x; i < (kMaxCand + 31) / 32; i += kSelThreads) taken[i] = 0u;
+      __syncthreads();
       if ((int)threadIdx.x < m) {
         const uint32_t mk = list_key[threadIdx.x], mi = list_id[threadIdx.x];
         int rank = 0;
-        for (int u = 0; u < m; ++u) {
-          const uint32_t uk = list_key[u];
-          rank += uk > mk || (uk == mk && list_id[u] < mi);
+#pragma unroll 8
+        for (int e = 0; e < m; ++e) {
+          const uint32_t ek = list_key[e];
+          rank += ek > mk || (ek == mk && list_id[e] < mi);
         }
-        keys[mi] = rank < need ? 0xffffffffu : 0u;
+        if (rank < need) atomicOr(&taken[mi >> 5], 1u << (mi & 31));
       }
       __syncthreads();
-      T = hi;
+      // A thread's run [i0, i0 + npt) spans at most two bitmap words.
+      const uint32_t w0 = taken[i0 >> 5];
+      const uint32_t w1 = ((i0 >> 5) + 1) < (kMaxCand + 31) / 32 ? taken[(i0 >> 5) + 1] : 0u;
+      const uint64_t bitsw = ((uint64_t)w1 << 32) | w0;
+      marked = (uint32_t)(bitsw >> (i0 & 31)) & ((npt >= 32) ? 0xffffffffu : ((1u << npt) - 1u));
+      T = hi;  // keys above are taken; keys in [lo, hi] are taken when marked
       need = 0;
       break;
     }
   }
 
   // ---- ordered compaction: ascending block id ----------------------------------------------------
-  const int chunk = (n + kSelThreads - 1) / kSelThreads;
-  const int i0 = min(n, (int)threadIdx.x * chunk), i1 = min(n, i0 + chunk);
+  // One scan of (ties, taken-above) counts; ties are taken in index order, so the ties before a
+  // thread that are taken number min(ties before, need).
   uint32_t gt = 0, eq = 0;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = keys[i];
-    gt += key > T;
-    eq += key == T;
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    if (live[u]) {
+      const bool m = (marked >> u) & 1u;
+      gt += key[u] > T || m;
+      eq += key[u] == T && !m;
+    }
   }
   uint32_t tot;
-  const uint32_t eq_before = block_exclusive_scan(eq, scan, &tot);
-  int take_eq = need - (int)eq_before;
+  const uint32_t packed = block_exclusive_scan((eq << 16) | gt, scan, &tot);
+  const int eq_before = (int)(packed >> 16), gt_before = (int)(packed & 0xffffu);
+  int take_eq = need - eq_before;
   take_eq = take_eq < 0 ? 0 : (take_eq > (int)eq ? (int)eq : take_eq);
-  uint32_t pos = block_exclusive_scan(gt + (uint32_t)take_eq, scan, &tot);
-  uint64_t* sortbuf = reinterpret_cast<uint64_t*>(hist);  // free after the passes
+  uint32_t pos = (uint32_t)gt_before + (uint32_t)min(eq_before, need);
+  uint64_t* sortbuf = reinterpret_cast<uint64_t*>(region);  // free after the passes
   int32_t* out_h = out_idx + (int64_t)h * idx_stride;
   int taken_eq = 0;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = keys[i];
-    const bool take = key > T || (key == T && taken_eq < take_eq);
-    if (key == T && take) ++taken_eq;
-    if (take) {
-      if (pos < (uint32_t)k) {  // exactly k are taken; the guard keeps a logic error in bounds
-        if (sorted) {
-          // keys[] may hold a taken marker: sort on the bound itself.
-          sortbuf[pos] = ((uint64_t)orderable(bound_h[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-        } else {
-          out_h[pos] = i + cand_offset;
-        }
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    if (live[u]) {
+      const int i = i0 + u;
+      bool take = key[u] > T || ((marked >> u) & 1u);
+      if (!take && key[u] == T && taken_eq < take_eq) {
+        take = true;
+        ++taken_eq;
       }
-      ++pos;
+      if (take) {
+        if (pos < (uint32_t)k) {  // exactly k are taken; the guard keeps a logic error in bounds
+          if (sorted) {
+            sortbuf[pos] = ((uint64_t)key[u] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+          } else {
+            out_h[pos] = i + cand_offset;
+          }
+        }
+        ++pos;
+      }
     }
   }
   if (!sorted) return;
@@ -332,37 +383,25 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
   }
 }
 
-// LDS words the select needs: the keys (padded to 4 words), then max(histogram, sort slots),
-// then the scan scratch.
-static size_t select_lds_words(int n_cand, int k, int sorted) {
-  size_t region = kBins;
-  if (sorted) {
-    size_t kp2 = 1;
-    while (kp2 < (size_t)k) kp2 <<= 1;
-    if (2 * kp2 > region) region = 2 * kp2;
-  }
-  return (size_t)((n_cand + 3) & ~3) + region + kScanWords;
-}
-
 template <int D, int MT, int G>
 int launch_bound(hipStream_t stream, const void* q, int q_dtype, const void* kmin, const void* kmax, int64_t mhs, int n_kv,
-                 int cand_offset, int n_cand, int rank_mode, float* bounds) {
+                 int cand_offset, int n_cand, int rank_mode, float* bounds, int64_t bstride) {
   using T = typename lkv::Elem<MT>::T;
   const int splits = (n_cand + kBlocksPerWG - 1) / kBlocksPerWG;
   hipLaunchKernelGGL((bound_kernel<D, MT, G>), dim3(splits * n_kv), dim3(kBoundThreads), 0, stream, q, q_dtype,
-                     (const T*)kmin, (const T*)kmax, mhs, n_kv, cand_offset, n_cand, rank_mode, bounds);
+                     (const T*)kmin, (const T*)kmax, mhs, n_kv, cand_offset, n_cand, rank_mode, bounds, bstride);
   LKV_CHECK_LAUNCH("bound");
   return LKV_OK;
 }
 
 template <int D, int MT>
 int dispatch_g(int g, hipStream_t s, const void* q, int qd, const void* kmin, const void* kmax, int64_t mhs, int n_kv,
-               int co, int nc, int rm, float* b) {
+               int co, int nc, int rm, float* b, int64_t bs) {
   switch (g) {
-    case 1: return launch_bound<D, MT, 1>(s, q, qd, kmin, kmax, mhs, n_kv, co, nc, rm, b);
-    case 2: return launch_bound<D, MT, 2>(s, q, qd, kmin, kmax, mhs, n_kv, co, nc, rm, b);
-    case 4: return launch_bound<D, MT, 4>(s, q, qd, kmin, kmax, mhs, n_kv, co, nc, rm, b);
-    case 8: return launch_bound<D, MT, 8>(s, q, qd, kmin, kmax, mhs, n_kv, co, nc, rm, b);
+    case 1: return launch_bound<D, MT, 1>(s, q, qd, kmin, kmax, mhs, n_kv, co, nc, rm, b, bs);
+    case 2: return launch_bound<D, MT, 2>(s, q, qd, kmin, kmax, mhs, n_kv, co, nc, rm, b, bs);
+    case 4: return launch_bound<D, MT, 4>(s, q, qd, kmin, kmax, mhs, n_kv, co, nc, rm, b, bs);
+    case 8: return launch_bound<D, MT, 8>(s, q, qd, kmin, kmax, mhs, n_kv, co, nc, rm, b, bs);
     default: lkv_set_error("unsupported GQA group size %d (1, 2, 4 or 8)", g); return LKV_ERR_UNSUPPORTED;
   }
 }
@@ -372,7 +411,7 @@ int dispatch_g(int g, hipStream_t s, const void* q, int qd, const void* kmin, co
 extern "C" size_t lkv_bound_topk_workspace_bytes(int n_kv, int n_cand, int k) {
   (void)k;
   if (n_kv <= 0 || n_cand <= 0) return 0;
-  return lkv_align_up((size_t)n_kv * n_cand * 4, 256);
+  return lkv_align_up((size_t)n_kv * lkv_align_up((size_t)n_cand, 4) * 4, 256);
 }
 
 extern "C" int lkv_bound_topk(uintptr_t stream, const void* q, int q_dtype, const void* kmin, const void* kmax,
@@ -392,40 +431,40 @@ extern "C" int lkv_bound_topk(uintptr_t stream, const void* q, int q_dtype, cons
   LKV_CHECK_ARG(k == 0 || (out_idx != nullptr && idx_stride >= k), "out_idx missing or idx_stride < k");
   const int sorted = (flags & LKV_SORTED) ? 1 : 0;
   if (k > 0 && n_cand > kMaxCand) {
-    lkv_set_error("%d candidate blocks exceed the in-LDS select limit %d", n_cand, kMaxCand);
+    lkv_set_error("%d candidate blocks exceed the per-head select limit %d", n_cand, kMaxCand);
     return LKV_ERR_UNSUPPORTED;
   }
   if (sorted && k > kMaxSortedK) {
     lkv_set_error("sorted selection supports k <= %d", kMaxSortedK);
     return LKV_ERR_UNSUPPORTED;
   }
-  const size_t lds_bytes = select_lds_words(n_cand, k, sorted) * 4;
-  if (k > 0 && lds_bytes > 65536) {
-    lkv_set_error("selection of k=%d among %d candidates needs more than 64 KiB of LDS", k, n_cand);
-    return LKV_ERR_UNSUPPORTED;
-  }
+  // Scratch bound rows are padded to 4 floats so the select can read them as 16-byte vectors;
+  // a caller's out_bound is dense [n_kv, n_cand].
   float* bounds = out_bound;
+  int64_t bstride = n_cand;
   if (bounds == nullptr) {
     const size_t need = lkv_bound_topk_workspace_bytes(n_kv, n_cand, k);
     LKV_CHECK_ARG(ws != nullptr && ws_bytes >= need, "workspace of %zu bytes needed, got %zu", need, ws_bytes);
+    LKV_CHECK_ARG(((uintptr_t)ws & 15) == 0, "workspace must be 16-byte aligned");
     bounds = (float*)ws;
+    bstride = (int64_t)lkv_align_up((size_t)n_cand, 4);
   }
   const int g = n_q / n_kv;
   hipStream_t s = (hipStream_t)stream;
   int rc;
   if (head_dim == 128) {
     rc = meta_dtype == LKV_BF16 ? dispatch_g<128, LKV_BF16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv,
-                                                             cand_offset, n_cand, rank_mode, bounds)
+                                                             cand_offset, n_cand, rank_mode, bounds, bstride)
                                 : dispatch_g<128, LKV_F16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv,
-                                                            cand_offset, n_cand, rank_mode, bounds);
+                                                            cand_offset, n_cand, rank_mode, bounds, bstride);
   } else {
     rc = meta_dtype == LKV_BF16 ? dispatch_g<64, LKV_BF16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv,
-                                                            cand_offset, n_cand, rank_mode, bounds)
+                                                            cand_offset, n_cand, rank_mode, bounds, bstride)
                                 : dispatch_g<64, LKV_F16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv,
-                                                           cand_offset, n_cand, rank_mode, bounds);
+                                                           cand_offset, n_cand, rank_mode, bounds, bstride);
   }
   if (rc != LKV_OK || k == 0) return rc;
-  hipLaunchKernelGGL(select_kernel, dim3(n_kv), dim3(kSelThreads), lds_bytes, s, bounds, n_cand, k, cand_offset,
+  hipLaunchKernelGGL(select_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k, cand_offset,
                      sorted, out_idx, idx_stride);
   LKV_CHECK_LAUNCH("select");
   return LKV_OK;
