@@ -235,6 +235,7 @@ def main() -> int:
         },
         "host_syncs_per_layer": 0,
     }
+    traffic = pmc_traffic()
     if want_zc:
         r = res["zerocopy"]
         pcie_gbps = B_sel / (r["dec_us"] * 1e-6) / 1e9
@@ -244,8 +245,10 @@ def main() -> int:
         out.update(value=round(r["us_layer"], 3), ms_per_step=round(r["ms_step"], 4))
         out["roofline"] = {
             "bound": "pcie", "kernel": "sparse_decode (zero-copy host reads)", "achieved": round(pcie_gbps, 2), "peak": PCIE_PEAK_GBPS,
-            "unit": "GB/s", "frac": round(pcie_gbps / PCIE_PEAK_GBPS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(pcie_gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get("zerocopy/sparse_decode_kernel"),
             "algorithmic_bytes": B_sel, "kernel_us": round(r["dec_us"], 2),
+            "traffic_note": "calibrated FETCH_SIZE + WRITE_SIZE bytes per launch, host (PCIe) and HBM fetches together; algorithmic total incl. HBM part "
+            f"{B_sel + B_sinkcur + B_q + B_out}; source {TRAFFIC_FILE.relative_to(ROOT)}" if traffic else None,
         }
         out["byte_roofline"] = {
             "hbm_bytes_per_layer": B_hbm_zc, "pcie_bytes_per_layer": B_sel,
@@ -276,7 +279,7 @@ def main() -> int:
             out.update(value=round(r["us_layer"], 3), ms_per_step=round(r["ms_step"], 4))
             out["config"]["workload"] = out["config"]["workload"].replace("bf16 KV in mapped pinned host memory", "bf16 KV resident in HBM")
             out["roofline"] = {"bound": "hbm", "kernel": "sparse_decode (HBM)", "achieved": round(dec_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                               "frac": round(dec_gbps / HBM_PEAK_GBPS, 4), "traffic": None, "algorithmic_bytes": B_sel + B_sinkcur + B_q + B_out, "kernel_us": round(r["dec_us"], 2)}
+                               "frac": round(dec_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get("hbm/sparse_decode_kernel"), "algorithmic_bytes": B_sel + B_sinkcur + B_q + B_out, "kernel_us": round(r["dec_us"], 2)}
     out["probes"] = {kk: round(v, 2) for kk, v in probe.items()}
 
     # ---- CPU baseline: the reference's decode path on this host's cores -----------------------------
@@ -284,6 +287,20 @@ def main() -> int:
         out["cpu_baseline"] = cpu_baseline(layers, k, n_sealed, fill, scale, args.cpu_seconds, outs, lses)
     print(json.dumps(out), flush=True)
     return 0
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "tiered_decode_128k_pmc_traffic.json"
+
+
+def pmc_traffic() -> dict:
+    """Calibrated HBM/fabric bytes per launch, per "<leg>/<kernel>", from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of this same workload (a counter run cannot time itself)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return {}
+    return {key: v["traffic_bytes"] for key, v in data.get("kernels", {}).items()}
 
 
 def cpu_baseline(layers: list, k: int, n_sealed: int, fill: int, scale: float, budget_s: float, outs: list, lses: list) -> dict:
