@@ -244,7 +244,7 @@ def main() -> int:
         t_roof_probe = max(B_hbm_zc / (HBM_PEAK_GBPS * 1e9), B_sel / (bw_probe * 1e9)) * 1e6 if bw_probe else None
         out.update(value=round(r["us_layer"], 3), ms_per_step=round(r["ms_step"], 4))
         out["roofline"] = {
-            "bound": "pcie", "kernel": "sparse_decode (zero-copy host reads)", "achieved": round(pcie_gbps, 2), "peak": PCIE_PEAK_GBPS,
+            "bound": "pcie", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, zero-copy host reads", "achieved": round(pcie_gbps, 2), "peak": PCIE_PEAK_GBPS,
             "unit": "GB/s", "frac": round(pcie_gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get("zerocopy/sparse_decode_kernel"),
             "algorithmic_bytes": B_sel, "kernel_us": round(r["dec_us"], 2),
             "traffic_note": "calibrated FETCH_SIZE + WRITE_SIZE bytes per launch, host (PCIe) and HBM fetches together; algorithmic total incl. HBM part "
@@ -278,7 +278,7 @@ def main() -> int:
         if not want_zc:
             out.update(value=round(r["us_layer"], 3), ms_per_step=round(r["ms_step"], 4))
             out["config"]["workload"] = out["config"]["workload"].replace("bf16 KV in mapped pinned host memory", "bf16 KV resident in HBM")
-            out["roofline"] = {"bound": "hbm", "kernel": "sparse_decode (HBM)", "achieved": round(dec_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            out["roofline"] = {"bound": "hbm", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, HBM", "achieved": round(dec_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                                "frac": round(dec_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get("hbm/sparse_decode_kernel"), "algorithmic_bytes": B_sel + B_sinkcur + B_q + B_out, "kernel_us": round(r["dec_us"], 2)}
     out["probes"] = {kk: round(v, 2) for kk, v in probe.items()}
 

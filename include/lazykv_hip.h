@@ -45,6 +45,8 @@ enum { LKV_SORTED = 1 };
 enum { LKV_RANK_F32 = 0, LKV_RANK_MODEL = 1 };
 /* lkv_host_alloc flags */
 enum { LKV_HOST_COHERENT = 1 };
+/* lkv_kv_source.flags */
+enum { LKV_SRC_HOST = 1 };
 
 /*
  * Where one set of KV blocks lives. Block b of KV head h has its key rows at
@@ -56,6 +58,9 @@ enum { LKV_HOST_COHERENT = 1 };
  * Layouts this describes: the host pool and GPU slot pool [blocks, h, 2, bs, d]
  * (lazykv/tiered.py:261,265), the int8 host pool [blocks, h, P], a full cache [1, h, T, d]
  * (lazykv/cache.py:35-36) and the exact tier's float32 mirror [h, T, d] (lazykv/exact.py:131-140).
+ * flags: LKV_SRC_HOST when the blocks are mapped host memory (read over PCIe). It changes only
+ * how a launch divides the work: host reads are issued from fewer workgroups, since the link
+ * serves a shallow queue of reads faster than a deep one. Results do not depend on it.
  */
 typedef struct lkv_kv_source {
   const void* k;
@@ -65,6 +70,7 @@ typedef struct lkv_kv_source {
   int64_t n_blocks;
   int32_t dtype;
   int32_t deq_dtype;
+  int32_t flags;
 } lkv_kv_source;
 
 /* Shape and sequence state of one decode-attention call. */

@@ -20,6 +20,7 @@ F16, BF16, F32, INT8_RECORD = 0, 1, 2, 3
 SORTED = 1
 RANK_F32, RANK_MODEL = 0, 1
 HOST_COHERENT = 1
+SRC_HOST = 1
 
 _DTYPE_CODES = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
 
@@ -42,6 +43,7 @@ class KVSource(ctypes.Structure):
         ("n_blocks", ctypes.c_int64),
         ("dtype", ctypes.c_int32),
         ("deq_dtype", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
     ]
 
 

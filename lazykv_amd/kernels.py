@@ -76,9 +76,14 @@ class Source:
     deq_dtype: int
     n_blocks: int
     owners: tuple = ()
+    flags: int = 0  # _lib.SRC_HOST for blocks in mapped host memory
 
     def c(self) -> _lib.KVSource:
-        return _lib.KVSource(self.k, self.v, self.block_stride, self.head_stride, self.n_blocks, self.dtype, self.deq_dtype)
+        return _lib.KVSource(self.k, self.v, self.block_stride, self.head_stride, self.n_blocks, self.dtype, self.deq_dtype, self.flags)
+
+
+def _location(t: torch.Tensor) -> int:
+    return 0 if t.is_cuda else _lib.SRC_HOST
 
 
 def pool_source(pool: torch.Tensor) -> Source:
@@ -89,7 +94,7 @@ def pool_source(pool: torch.Tensor) -> Source:
     base = address(pool)
     es = pool.element_size()
     code = _lib.dtype_code(pool.dtype)
-    return Source(base, base + bs * d * es, h * 2 * bs * d, 2 * bs * d, code, code, pool.shape[0], (pool,))
+    return Source(base, base + bs * d * es, h * 2 * bs * d, 2 * bs * d, code, code, pool.shape[0], (pool,), _location(pool))
 
 
 def record_source(records: torch.Tensor, deq_dtype: torch.dtype) -> Source:
@@ -98,7 +103,7 @@ def record_source(records: torch.Tensor, deq_dtype: torch.dtype) -> Source:
         raise ValueError(f"expected contiguous uint8 records [blocks, h, P], got {tuple(records.shape)} {records.dtype}")
     _, h, p = records.shape
     base = address(records)
-    return Source(base, 0, h * p, p, _lib.INT8_RECORD, _lib.dtype_code(deq_dtype), records.shape[0], (records,))
+    return Source(base, 0, h * p, p, _lib.INT8_RECORD, _lib.dtype_code(deq_dtype), records.shape[0], (records,), _location(records))
 
 
 def dense_source(keys: torch.Tensor, values: torch.Tensor, block_size: int) -> Source:
@@ -116,7 +121,7 @@ def dense_source(keys: torch.Tensor, values: torch.Tensor, block_size: int) -> S
     if k.stride(0) != v.stride(0):
         raise ValueError("keys and values must share their head stride")
     code = _lib.dtype_code(k.dtype)
-    return Source(address(k), address(v), block_size * d, k.stride(0), code, code, k.shape[1] // block_size, (keys, values))
+    return Source(address(k), address(v), block_size * d, k.stride(0), code, code, k.shape[1] // block_size, (keys, values), _location(k))
 
 
 # -- a1 + a2: bound and top-K -----------------------------------------------------------------------
