@@ -29,7 +29,10 @@ from typing import Any
 import numpy as np
 import torch
 
+from transformers.cache_utils import Cache
+
 from lazykv_amd import _lib, kernels
+from lazykv_amd.cache import FullGPUCache
 from lazykv_amd.pinned import pinned_empty
 from lazykv_amd.quant import packed_pair_bytes
 from lazykv_amd.selection import QUEST_DENSE_LAYERS
@@ -280,20 +283,24 @@ class TieredLayer:
         return self.n_sealed * self.h * self.pair_bytes if self.host is not None else 0
 
 
-class TieredCache:
-    """Decode-time cache: dense layers are the caller's, selecting layers are tiered (lazykv/tiered.py:538-747).
+class TieredCache(Cache):
+    """Decode-time cache: dense layers share the prefilled FullGPUCache, selecting layers are
+    tiered (lazykv/tiered.py:538-747).
 
-    Build it from prefilled per-layer KV (`layers`: list of (keys, values) [1, h, L, d] on the GPU)
-    or from prebuilt `tiers`. `select` returns a `Decoded` (the finished attention of the step), or
-    None to attend densely (dense layers, multi-token forwards).
+    `full` is the exactly prefilled cache (a FullGPUCache, or a list of per-layer (keys, values)
+    [1, h, L, d] on the GPU, which is copied into one). Its first `dense_layers` layers stay in it
+    and keep growing during decode; every other layer becomes a TieredLayer, unless `tiers` brings
+    them prebuilt (the layer-major prefill, which never holds them in `full`). `select` returns a
+    `Decoded` (the finished attention of the step), or None to attend densely.
     """
 
     def __init__(
         self,
-        layers: list[tuple[torch.Tensor, torch.Tensor]] | None,
+        full: FullGPUCache | list[tuple[torch.Tensor, torch.Tensor]],
         k_blocks: int,
         block_size: int,
         capacity_tokens: int,
+        model: Any = None,
         dense_layers: int = QUEST_DENSE_LAYERS,
         host_pools: list[torch.Tensor] | None = None,
         n_slots: int | None = None,
@@ -306,6 +313,9 @@ class TieredCache:
         record_selection: bool = False,
         replay_selection: Any = None,
     ) -> None:
+        if not isinstance(full, FullGPUCache):
+            full = FullGPUCache.from_kv(list(full), capacity_tokens)
+        super().__init__(layers=full.layers)
         if fetch not in FETCH_MODES:
             raise ValueError(f"unknown fetch mode {fetch!r}")
         if fetch == "zerocopy" and (prefetch or record_selection or replay_selection is not None):
@@ -316,17 +326,17 @@ class TieredCache:
         self.k_blocks, self.block_size, self.dense_layers = k_blocks, block_size, dense_layers
         self.fetch, self.quant, self.exact = fetch, quant, exact
         self.counters = TierCounters()
-        self.dense: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+        self.full = full
+        n_layers = len(full.layers)
         if tiers is None:
-            if layers is None:
-                raise ValueError("need prefilled layers or prebuilt tiers")
             tiers = {}
-            for i in range(dense_layers, len(layers)):
-                k, v = layers[i]
+            for i in range(dense_layers, n_layers):
+                src = full.layers[i]
+                n = src.get_seq_length()
                 host = None if host_pools is None else host_pools[i - dense_layers]
-                tiers[i] = TieredLayer(k, v, k_blocks, block_size, capacity_tokens, host, n_slots, quant=quant, fetch=fetch, exact=exact, rank_dtype=rank_dtype)
-            for i in range(min(dense_layers, len(layers))):
-                self.dense[i] = layers[i]
+                tiers[i] = TieredLayer(src.keys[:, :, :n], src.values[:, :, :n], k_blocks, block_size, capacity_tokens, host, n_slots, quant=quant, fetch=fetch, exact=exact, rank_dtype=rank_dtype)
+        elif sorted(tiers) != list(range(dense_layers, n_layers)):
+            raise ValueError(f"prebuilt tiers must cover layers {dense_layers}..{n_layers - 1}, got {sorted(tiers)}")
         self.tiers = tiers
         for t in tiers.values():
             self.counters.boundary_d2h_bytes += t.boundary_d2h_bytes
@@ -342,7 +352,7 @@ class TieredCache:
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, *args: object, **kwargs: object) -> tuple[torch.Tensor, torch.Tensor]:
         tier = self.tiers.get(layer_idx)
         if tier is None:
-            raise RuntimeError(f"layer {layer_idx} is dense; its KV belongs to the caller's cache")
+            return self.full.layers[layer_idx].update(key_states, value_states)
         if key_states.shape[-2] != 1:
             raise NotImplementedError("multi-token ingestion into the tier is outside the decode path")
         tier.append(key_states, value_states, self.counters)
@@ -350,10 +360,7 @@ class TieredCache:
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
         tier = self.tiers.get(layer_idx)
-        if tier is not None:
-            return tier.length
-        k, _ = self.dense[layer_idx]
-        return k.shape[2]
+        return tier.length if tier is not None else self.full.layers[layer_idx].get_seq_length()
 
     def model_kwargs(self) -> dict[str, object]:
         return {"lazykv_selector": self}
