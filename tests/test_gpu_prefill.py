@@ -133,3 +133,50 @@ def test_prompt_longer_than_capacity_is_refused(tiny) -> None:  # noqa: ANN001
     cfg, model = tiny
     with pytest.raises(ValueError, match="exceeds capacity"):
         tiered_prefill(model, _ids(cfg)[:, :PROMPT], 32, K, BS, capacity_tokens=64, dense_layers=1)
+
+
+@torch.inference_mode()
+def test_layer_major_prefill_32k_1b_shape_writes_quant_py_records() -> None:
+    """The 1B-shaped prefill at its real size: 16 layers (hidden 2048, 32/8 heads, d 64), float16
+    weights ~ N(0, 0.02) with unit RMSNorm gains, a 32,768-token prompt uniform over 128,256 ids,
+    every layer's KV straight into the int8 host tier. A sample of each layer's records equals
+    quant.py's pack of the chunk-major prefill's KV, and their metadata the min/max of unpack."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from lazykv_amd.attention import IMPLEMENTATION_NAME, install
+    from lazykv_amd.cache import FullGPUCache
+    from lazykv_amd.tiered_prefill import tiered_prefill
+
+    install()
+    n, chunk, bs, d, k = 32768, 4096, 16, 64, 512
+    cfg = LlamaConfig(hidden_size=2048, intermediate_size=8192, num_hidden_layers=16, num_attention_heads=32, num_key_value_heads=8, head_dim=d,
+                      vocab_size=128256, max_position_embeddings=131072, rope_theta=500000.0, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = LlamaForCausalLM(cfg)
+    model.set_attn_implementation(IMPLEMENTATION_NAME)
+    model = model.to(dtype=torch.float16).eval()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    ids = torch.randint(0, cfg.vocab_size, (1, n), device="cuda", generator=gen)
+    got = tiered_prefill(model, ids, chunk, k, bs, n + 64, dense_layers=0, quant="int8")
+    full = FullGPUCache(cfg.num_hidden_layers, n)
+    out = None
+    for s in range(0, n, chunk):
+        out = model(input_ids=ids[:, s : s + chunk], past_key_values=full, use_cache=True, logits_to_keep=1)
+    assert torch.equal(got.last_logits, out.logits[0, -1].float())
+    assert not any(layer.is_initialized for layer in got.full.layers)
+    nb = n // bs
+    rng = np.random.default_rng(5)
+    for i, t in got.cache.tiers.items():
+        assert (t.n_sealed, t.fill) == (nb, 0)
+        blocks = rng.integers(0, nb, 64)
+        heads = rng.integers(0, cfg.num_key_value_heads, 64)
+        kb = _bits(full.layers[i].keys[0])  # [h, n, d]
+        vb = _bits(full.layers[i].values[0])
+        pairs = np.stack([np.stack([kb[h, b * bs : (b + 1) * bs], vb[h, b * bs : (b + 1) * bs]]) for b, h in zip(blocks, heads)])  # [64, 2, bs, d]
+        want = R.pack(pairs, "f16")
+        assert np.array_equal(t.host[torch.from_numpy(blocks), torch.from_numpy(heads)].numpy(), want), i
+        keys = R.to_f32(R.unpack(want, bs, d, "f16"), "f16")[:, 0]  # [64, bs, d]
+        assert np.array_equal(_bits(t.kmin[0][torch.from_numpy(heads).cuda(), torch.from_numpy(blocks).cuda()]), R.from_f32(keys.min(axis=1), "f16"))
+        assert np.array_equal(_bits(t.kmax[0][torch.from_numpy(heads).cuda(), torch.from_numpy(blocks).cuda()]), R.from_f32(keys.max(axis=1), "f16"))
+    print(f"tiered prefill 32K x 16 layers: wall {got.wall_s:.3f} s, tier builds {got.boundary_s * 1e3:.2f} ms in all")
