@@ -1,20 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark: the Llama-3.1-8B-shaped tiered decode step at 131,072 tokens and a 6.25% budget.
+"""Benchmark of the tiered decode-attention path on one MI355X; prints one JSON line.
 
-Workload (per decode step, 32 selecting layers): 32 query / 8 KV heads, head_dim 128, bf16 KV,
-16-token blocks, 8,192 blocks per KV head of which 8,190 are candidates; K = 512 selected per KV
-head. Every layer's KV lives in mapped pinned host memory (512 MiB per layer, 16 GiB in all); the
-block metadata, the sink and the current block live in HBM. Per layer, one step runs the fused
-Quest bound + top-K kernel over the metadata and the block-sparse decode kernel, which reads the
-4,096 selected (block, head) pairs in place over PCIe. Nothing returns to the host between
-layers. The 32-layer step is captured once in a HIP graph and replayed.
+Default workload (`--workload decode128k`): the Llama-3.1-8B-shaped tiered decode step at
+131,072 tokens and a 6.25% budget. Per decode step, 32 selecting layers: 32 query / 8 KV heads,
+head_dim 128, bf16 KV, 16-token blocks, 8,192 blocks per KV head of which 8,190 are candidates;
+K = 512 selected per KV head. Every layer's KV lives in mapped pinned host memory (512 MiB per
+layer, 16 GiB in all); the block metadata, the sink and the current block live in HBM. Per
+layer, one step runs the Quest bound + top-K kernels over the metadata and the block-sparse
+decode kernels, which read the 4,096 selected (block, head) pairs in place over PCIe. Nothing
+returns to the host between layers. The 32-layer step is captured once in a HIP graph and
+replayed. `value` = decode-step microseconds per layer (lower is better); beside it the same step
+with the KV resident in HBM, per-kernel durations against the byte roofline, the link probe, and
+the reference's CPU decode path (`oracle/cpu_path.py`) timed on this host on a bounded sample.
 
-Reported: `value` = decode-step microseconds per layer (lower is better). Beside it: the same
-step with all KV resident in HBM, per-kernel durations and their achieved bandwidth against the
-byte roofline, the link probe, and the reference's CPU decode path (`oracle/cpu_path.py`) timed on
-this host's cores on a bounded sample of layers.
+Other workloads (same JSON contract, for the parity-test configurations):
+  decode32k  -- Llama-3.2-1B-shaped decode, 32,768 tokens, d 64, float16, K 512, all in HBM
+                (16 seeded layer instances, rotated so the 256 MB last-level cache cannot hold them)
+  int8_64k   -- 1B-shaped, 16 layers, 65,536 tokens, d 64, float16, K 1,024, sealed blocks as int8
+                records (`--tier-where hbm|host`), dequantised in the decode load
+  exact128k  -- 8B-shaped exact split, 32 layers, 131,072 tokens: K of 512 / 2,048 / 4,096 from the
+                exact HBM store, every other sealed block from the int8 host tier, merged by LSE
+  prefill32k -- 1B-shaped layer-major prefill of a 32,768-token prompt, 16 layers, float16, every
+                layer's KV turned into the int8 host tier by the fused pack + metadata kernel
 
-    python bench.py [--steps K] [--warmup W] [--layers 32] [--no-cpu-baseline] [--only zerocopy|hbm]
+    python bench.py [--workload W] [--steps K] [--warmup W] [--layers L] [--no-cpu-baseline]
 """
 
 from __future__ import annotations
@@ -33,6 +42,16 @@ sys.path.insert(0, str(ROOT))
 METRIC = "decode-step µs/layer & achieved HBM GB/s (% roofline) at 128K ctx, 6.25% budget"
 HBM_PEAK_GBPS = 8000.0
 PCIE_PEAK_GBPS = 64.0  # PCIe Gen5 x16, one direction
+N_Q, H, BS = 32, 8, 16
+TRAFFIC_FILE = ROOT / "profiles" / "tiered_decode_128k_pmc_traffic.json"
+
+WORKLOADS = {
+    "decode128k": dict(layers=32, tokens=131072, d=128, dtype="bfloat16", k=(512,), kind="host"),
+    "decode32k": dict(layers=16, tokens=32768, d=64, dtype="float16", k=(512,), kind="hbm"),
+    "int8_64k": dict(layers=16, tokens=65536, d=64, dtype="float16", k=(1024,), kind="int8"),
+    "exact128k": dict(layers=32, tokens=131072, d=128, dtype="bfloat16", k=(512, 2048, 4096), kind="exact"),
+    "prefill32k": dict(layers=16, tokens=32768, d=64, dtype="float16", k=(512,), kind="prefill"),
+}
 
 
 def log(msg: str) -> None:
@@ -42,259 +61,106 @@ def log(msg: str) -> None:
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="decode128k")
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--layers", type=int, default=32)
-    p.add_argument("--tokens", type=int, default=131072)
-    p.add_argument("--k", type=int, default=512)
+    p.add_argument("--layers", type=int, default=None)
+    p.add_argument("--tokens", type=int, default=None)
+    p.add_argument("--k", type=int, default=None, help="selected blocks per KV head (default: the workload's)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["zerocopy", "hbm"], default=None)
+    p.add_argument("--only", choices=["zerocopy", "hbm"], default=None, help="decode128k: one leg only")
+    p.add_argument("--tier-where", choices=["hbm", "host"], default="hbm", help="int8_64k: where the int8 records live")
     p.add_argument("--eager", action="store_true", help="launch from Python instead of replaying a graph")
     p.add_argument("--coherent", action="store_true", help="fine-grained (device-uncached) host pools")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path has no multi-GPU mode (asked for --gpus {args.gpus}).", file=sys.stderr)
         return 2
-
-    import torch
-
-    from lazykv_amd import kernels
-    from lazykv_amd.pinned import device_address, pinned_empty
-    from lazykv_amd.workload import draw_layer, to_pool
-
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    n_q, h, d, bs, k = 32, 8, 128, 16, args.k
-    T, L = args.tokens, args.layers
-    N = T // bs
-    n_sealed, fill = N - 1, bs  # lazy sealing: the last block is the current one, full
-    n_cand = n_sealed - 1
-    scale = d**-0.5
-    want_zc = args.only in (None, "zerocopy")
-    want_hbm = args.only in (None, "hbm")
-
-    # ---- state -------------------------------------------------------------------------------
-    t0 = time.time()
-    layers = []
-    for li in range(L):
-        w = draw_layer(li, n_q, h, d, T, bs, torch.bfloat16, device=dev)
-        pool = to_pool(w.keys, w.values, bs)  # [N, h, 2, bs, d] on the GPU
-        kmin = torch.zeros((1, h, N, d), dtype=torch.bfloat16, device=dev)
-        kmax = torch.zeros_like(kmin)
-        kernels.store_blocks(kernels.dense_source(w.keys, w.values, bs), n_kv=h, head_dim=d, block_size=bs, first_block=0, n_blocks=n_sealed, kmin=kmin, kmax=kmax)
-        slots = pool[[0, N - 1]].contiguous()
-        host = None
-        if want_zc:
-            host = pinned_empty(tuple(pool.shape), torch.bfloat16, coherent=args.coherent)
-            host.copy_(pool)
-        layers.append({"q": w.query.contiguous(), "kmin": kmin, "kmax": kmax, "slots": slots, "host": host, "pool": pool if want_hbm else None, "needle": w.needle})
-        del w
-        if not want_hbm:
-            del pool
-        if li % 8 == 7:
-            log(f"built {li + 1}/{L} layers ({time.time() - t0:.1f}s)")
-    torch.cuda.synchronize()
-    log(f"state ready in {time.time() - t0:.1f}s: {L} layers x {N} blocks, host pools {'yes' if want_zc else 'no'}, HBM pools {'yes' if want_hbm else 'no'}")
-
-    idx = torch.empty((h, k), dtype=torch.int32, device=dev)
-    ws_sel, ws_dec = kernels.Workspace(dev), kernels.Workspace(dev)
-    outs = [torch.empty((n_q, d), dtype=torch.bfloat16, device=dev) for _ in range(L)]
-    lses = [torch.empty((n_q,), dtype=torch.float32, device=dev) for _ in range(L)]
-    ranks, decodes = [], {"zerocopy": [], "hbm": []}
-    for li, st in enumerate(layers):
-        ranks.append(kernels.PreparedBoundTopk(st["q"], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx, ws=ws_sel))
-        ss = kernels.pool_source(st["slots"])
-        common = dict(n_kv=h, block_size=bs, scale=scale, idx=idx, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=fill, out=outs[li], lse=lses[li], ws=ws_dec)
-        if want_zc:
-            decodes["zerocopy"].append(kernels.PreparedDecode(st["q"], sel=kernels.pool_source(st["host"]), **common))
-        if want_hbm:
-            decodes["hbm"].append(kernels.PreparedDecode(st["q"], sel=kernels.pool_source(st["pool"]), **common))
-
-    def step(mode: str) -> None:
-        for li in range(L):
-            ranks[li]()
-            decodes[mode][li]()
-
-    def check(mode: str) -> None:
-        """Every layer's needle is selected for every KV head; outputs are finite."""
-        for li in range(L):
-            ranks[li]()
-            got = idx.cpu()
-            needle = layers[li]["needle"]
-            assert (got == needle).any(dim=1).all(), f"layer {li}: needle block {needle} not selected"
-            decodes[mode][li]()
-        torch.cuda.synchronize()
-        assert all(torch.isfinite(o.float()).all() for o in outs), "non-finite output"
-
-    def time_mode(mode: str) -> dict:
-        check(mode)
-        step(mode)
-        torch.cuda.synchronize()
-        graph = None
-        if not args.eager:
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                step(mode)
-            torch.cuda.synchronize()
-        run = graph.replay if graph is not None else (lambda: step(mode))
-        for _ in range(args.warmup):
-            run()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        wall0 = time.perf_counter()
-        e0.record()
-        for _ in range(args.steps):
-            run()
-        e1.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - wall0
-        ms_step = e0.elapsed_time(e1) / args.steps
-        # Per-kernel durations, eager, with events on the launch stream bracketing each kernel.
-        sel_ms, dec_ms = [], []
-        for _ in range(max(2, min(5, args.steps))):
-            for li in range(L):
-                a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-                a.record()
-                ranks[li]()
-                b.record()
-                decodes[mode][li]()
-                c.record()
-                sel_ms.append((a, b))
-                dec_ms.append((b, c))
-        torch.cuda.synchronize()
-        sel_us = statistics.mean(x.elapsed_time(y) for x, y in sel_ms) * 1e3
-        dec_us = statistics.mean(x.elapsed_time(y) for x, y in dec_ms) * 1e3
-        eager_us = None
-        if graph is not None:
-            torch.cuda.synchronize()
-            w0 = time.perf_counter()
-            for _ in range(3):
-                step(mode)
-            torch.cuda.synchronize()
-            eager_us = (time.perf_counter() - w0) / 3 / L * 1e6
-            del graph
-        log(f"{mode}: {ms_step:.3f} ms/step = {ms_step * 1e3 / L:.1f} us/layer (bound+topk {sel_us:.1f} us, decode {dec_us:.1f} us), wall {wall:.2f}s")
-        return {"ms_step": ms_step, "us_layer": ms_step * 1e3 / L, "sel_us": sel_us, "dec_us": dec_us, "eager_us_layer": eager_us}
-
-    # ---- algorithmic bytes per layer (kernel-level) --------------------------------------------
-    B_meta = 2 * h * n_cand * d * 2
-    B_q = n_q * d * 2
-    B_out = n_q * d * 2 + 4 * n_q
-    B_sel = 2 * h * k * bs * d * 2
-    B_sinkcur = 2 * h * 2 * bs * d * 2
-    B_hbm_zc = B_meta + B_sinkcur + 2 * B_q + B_out  # q is read by both kernels
-
-    res = {}
-    if want_zc:
-        res["zerocopy"] = time_mode("zerocopy")
-    if want_hbm:
-        res["hbm"] = time_mode("hbm")
-
-    # ---- link and HBM probes ---------------------------------------------------------------------
-    probe = {}
-    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
-
-    def probe_gbps(addr: int, nbytes: int, blocks: int, reps: int = 5) -> float:
-        kernels.stream_read(addr, nbytes, blocks, sink)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            kernels.stream_read(addr, nbytes, blocks, sink)
-        e1.record()
-        torch.cuda.synchronize()
-        return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
-
-    if want_zc:
-        host0 = layers[0]["host"]
-        probe["pcie_read_gbps"] = probe_gbps(device_address(host0), host0.numel() * 2, 2048)
-    big = torch.empty(4 << 30, dtype=torch.uint8, device=dev)
-    probe["hbm_read_gbps"] = probe_gbps(big.data_ptr(), big.numel(), 4096)
-    del big
-    log(f"probes: {probe}")
-
-    out = {
-        "metric": METRIC,
-        "value": None,
-        "unit": "us/layer",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": None,
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": f"Llama-3.1-8B-shaped tiered decode step: {L} selecting layers, {T} tokens, 16-token blocks, K={k} of {n_cand} candidates per KV head (6.25% budget), bf16 KV in mapped pinned host memory",
-            "layers": L, "tokens": T, "q_heads": n_q, "kv_heads": h, "head_dim": d, "block_size": bs, "k": k,
-            "rank_dtype": "float32", "dense_layers": 0, "launch": "eager" if args.eager else "hip_graph",
-            "host_memory": "fine-grained" if args.coherent else "coarse-grained",
-        },
-        "host_syncs_per_layer": 0,
-    }
-    traffic = pmc_traffic()
-    if want_zc:
-        r = res["zerocopy"]
-        pcie_gbps = B_sel / (r["dec_us"] * 1e-6) / 1e9
-        t_roof64 = max((B_hbm_zc) / (HBM_PEAK_GBPS * 1e9), B_sel / (PCIE_PEAK_GBPS * 1e9)) * 1e6
-        bw_probe = probe.get("pcie_read_gbps")
-        t_roof_probe = max(B_hbm_zc / (HBM_PEAK_GBPS * 1e9), B_sel / (bw_probe * 1e9)) * 1e6 if bw_probe else None
-        out.update(value=round(r["us_layer"], 3), ms_per_step=round(r["ms_step"], 4))
-        out["roofline"] = {
-            "bound": "pcie", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, zero-copy host reads", "achieved": round(pcie_gbps, 2), "peak": PCIE_PEAK_GBPS,
-            "unit": "GB/s", "frac": round(pcie_gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get("zerocopy/sparse_decode_kernel"),
-            "algorithmic_bytes": B_sel, "kernel_us": round(r["dec_us"], 2),
-            "traffic_note": "calibrated FETCH_SIZE + WRITE_SIZE bytes per launch, host (PCIe) and HBM fetches together; algorithmic total incl. HBM part "
-            f"{B_sel + B_sinkcur + B_q + B_out}; source {TRAFFIC_FILE.relative_to(ROOT)}" if traffic else None,
-        }
-        out["byte_roofline"] = {
-            "hbm_bytes_per_layer": B_hbm_zc, "pcie_bytes_per_layer": B_sel,
-            "t_roof_us_at_64gbps": round(t_roof64, 2), "frac_at_64gbps": round(t_roof64 / r["us_layer"], 4),
-            "t_roof_us_at_probe": round(t_roof_probe, 2) if t_roof_probe else None,
-            "frac_at_probe": round(t_roof_probe / r["us_layer"], 4) if t_roof_probe else None,
-        }
-        out["kernels"] = {
-            "bound_topk": {"us": round(r["sel_us"], 2), "hbm_bytes": B_meta + B_q, "gbps": round((B_meta + B_q) / (r["sel_us"] * 1e-6) / 1e9, 1),
-                           "frac_hbm_peak": round((B_meta + B_q) / (r["sel_us"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)},
-            "sparse_decode": {"us": round(r["dec_us"], 2), "pcie_bytes": B_sel, "hbm_bytes": B_sinkcur + B_q + B_out, "pcie_gbps": round(pcie_gbps, 2)},
-        }
-        out["eager_us_per_layer"] = round(r["eager_us_layer"], 2) if r["eager_us_layer"] else None
-    if want_hbm:
-        r = res["hbm"]
-        b_hbm = B_meta + B_sel + B_sinkcur + 2 * B_q + B_out
-        t_roof = b_hbm / (HBM_PEAK_GBPS * 1e9) * 1e6
-        dec_gbps = (B_sel + B_sinkcur + B_q + B_out) / (r["dec_us"] * 1e-6) / 1e9
-        sel_gbps = (B_meta + B_q) / (r["sel_us"] * 1e-6) / 1e9
-        out["hbm_resident"] = {
-            "us_per_layer": round(r["us_layer"], 3), "ms_per_step": round(r["ms_step"], 4), "hbm_bytes_per_layer": b_hbm,
-            "t_roof_us": round(t_roof, 3), "frac": round(t_roof / r["us_layer"], 4),
-            "bound_topk_us": round(r["sel_us"], 2), "bound_topk_gbps": round(sel_gbps, 1),
-            "sparse_decode_us": round(r["dec_us"], 2), "sparse_decode_gbps": round(dec_gbps, 1),
-            "eager_us_per_layer": round(r["eager_us_layer"], 2) if r["eager_us_layer"] else None,
-        }
-        if not want_zc:
-            out.update(value=round(r["us_layer"], 3), ms_per_step=round(r["ms_step"], 4))
-            out["config"]["workload"] = out["config"]["workload"].replace("bf16 KV in mapped pinned host memory", "bf16 KV resident in HBM")
-            out["roofline"] = {"bound": "hbm", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, HBM", "achieved": round(dec_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                               "frac": round(dec_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get("hbm/sparse_decode_kernel"), "algorithmic_bytes": B_sel + B_sinkcur + B_q + B_out, "kernel_us": round(r["dec_us"], 2)}
-    out["probes"] = {kk: round(v, 2) for kk, v in probe.items()}
-
-    # ---- CPU baseline: the reference's decode path on this host's cores -----------------------------
-    if not args.no_cpu_baseline and want_zc:
-        out["cpu_baseline"] = cpu_baseline(layers, k, n_sealed, fill, scale, args.cpu_seconds, outs, lses)
+    spec = dict(WORKLOADS[args.workload])
+    spec["layers"] = args.layers or spec["layers"]
+    spec["tokens"] = args.tokens or spec["tokens"]
+    if args.k:
+        spec["k"] = (args.k,)
+    out = run_prefill(args, spec) if spec["kind"] == "prefill" else run_decode(args, spec)
     print(json.dumps(out), flush=True)
     return 0
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "tiered_decode_128k_pmc_traffic.json"
+# -- shared timing --------------------------------------------------------------------------------
+
+
+def _events(n: int):  # noqa: ANN202
+    import torch
+
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def time_step(step, steps: int, warmup: int, eager: bool) -> tuple[float, float]:  # noqa: ANN001
+    """(ms per step, wall s): `step` captured once in a HIP graph and replayed, or launched eagerly."""
+    import torch
+
+    step()
+    torch.cuda.synchronize()
+    graph = None
+    if not eager:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+    run = graph.replay if graph is not None else step
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    wall0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    del graph
+    return e0.elapsed_time(e1) / steps, wall
+
+
+def kernel_us(calls: list, reps: int) -> list[float]:
+    """Mean duration of each callable, launched eagerly, bracketed by events on the launch stream."""
+    import torch
+
+    marks = []
+    for _ in range(reps):
+        ev = _events(len(calls) + 1)
+        ev[0].record()
+        for i, c in enumerate(calls):
+            c()
+            ev[i + 1].record()
+        marks.append(ev)
+    torch.cuda.synchronize()
+    return [statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in marks) * 1e3 for i in range(len(calls))]
+
+
+def probe_gbps(addr: int, nbytes: int, blocks: int, reps: int = 5) -> float:
+    """The link (or HBM) asymptote: a streaming read of `nbytes` at a device-visible address."""
+    import torch
+
+    from lazykv_amd import kernels
+
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    kernels.stream_read(addr, nbytes, blocks, sink)
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    e0.record()
+    for _ in range(reps):
+        kernels.stream_read(addr, nbytes, blocks, sink)
+    e1.record()
+    torch.cuda.synchronize()
+    return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
 
 def pmc_traffic() -> dict:
     """Calibrated HBM/fabric bytes per launch, per "<leg>/<kernel>", from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary of this same workload (a counter run cannot time itself)."""
+    FETCH_SIZE / WRITE_SIZE summary of the default workload (a counter run cannot time itself)."""
     try:
         with open(TRAFFIC_FILE) as f:
             data = json.load(f)
@@ -303,57 +169,411 @@ def pmc_traffic() -> dict:
     return {key: v["traffic_bytes"] for key, v in data.get("kernels", {}).items()}
 
 
-def cpu_baseline(layers: list, k: int, n_sealed: int, fill: int, scale: float, budget_s: float, outs: list, lses: list) -> dict:
+def cpu_cores() -> tuple[int, int]:
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(16, avail)), avail
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        return ""
+
+
+def time_cpu(fn, states: list, budget_s: float) -> dict:  # noqa: ANN001
+    """Median seconds of `fn(*state)` over rotating states, at 8 threads and at the core count."""
     import torch
 
-    from oracle.cpu_path import decode_layer
-
-    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    cores = max(1, min(16, avail))
+    cores, avail = cpu_cores()
     settings = sorted({min(8, cores), cores})
     prev = torch.get_num_threads()
     results = {}
-    n_layers = min(len(layers), 8)
-    cpu_state = []
-    for st in layers[:n_layers]:
-        cpu_state.append((st["q"].cpu(), st["kmin"].cpu(), st["kmax"].cpu(), st["host"], st["slots"][0].cpu(), st["slots"][1].cpu()))
-    # Parity sanity: the CPU path and the GPU kernels on layer 0.
-    q, kmin, kmax, host, sink, cur = cpu_state[0]
-    o_cpu, l_cpu, _ = decode_layer(q, kmin, kmax, n_sealed, k, host, sink, cur, fill, scale)
-    gpu_diff = float((o_cpu - outs[0].float().cpu()).abs().max())
-    lse_diff = float((l_cpu - lses[0].cpu()).abs().max())
     for n in settings:
         torch.set_num_threads(n)
-        decode_layer(*cpu_state[0][:3], n_sealed, k, *cpu_state[0][3:], fill, scale)  # warmup
-        times = []
-        t_start = time.perf_counter()
-        i = 0
+        fn(*states[0])  # warmup
+        times, i, t_start = [], 0, time.perf_counter()
         while (time.perf_counter() - t_start) < budget_s / len(settings) or len(times) < 3:
-            q, kmin, kmax, host, sink, cur = cpu_state[i % n_layers]
             t0 = time.perf_counter()
-            decode_layer(q, kmin, kmax, n_sealed, k, host, sink, cur, fill, scale)
+            fn(*states[i % len(states)])
             times.append(time.perf_counter() - t0)
             i += 1
         results[n] = times
-        log(f"cpu baseline, {n} threads: median {statistics.median(times) * 1e3:.2f} ms/layer over {len(times)} layers")
+        log(f"cpu baseline, {n} threads: median {statistics.median(times) * 1e3:.2f} ms over {len(times)} runs")
     torch.set_num_threads(prev)
-    best_n = cores
-    med = statistics.median(results[best_n]) * 1e6
-    q1, _, q3 = statistics.quantiles(results[best_n], n=4) if len(results[best_n]) >= 4 else (med, med, med)
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
-    except OSError:
-        pass
-    return {
-        "value": round(med, 1), "unit": "us/layer", "cores": best_n, "kind": "port",
-        "sample": f"{sum(len(v) for v in results.values())} single-layer decodes of the same workload (layers 0-{n_layers - 1}, median over {len(results[best_n])} at {best_n} threads), torch CPU ops in the reference's order: fp32 quest bound, topk, index_select gather from the host pool, cat, masked fp32 attention + logsumexp",
-        "iqr_us": [round(q1 * 1e6, 1), round(q3 * 1e6, 1)] if len(results[best_n]) >= 4 else None,
-        "per_thread_setting_us": {str(n): round(statistics.median(v) * 1e6, 1) for n, v in results.items()},
-        "cpu_model": cpu_model, "host_cpus_visible": avail,
-        "gpu_vs_cpu_layer0_max_abs_out": gpu_diff, "gpu_vs_cpu_layer0_max_abs_lse": lse_diff,
+    t = results[cores]
+    med = statistics.median(t)
+    q1, _, q3 = statistics.quantiles(t, n=4) if len(t) >= 4 else (med, med, med)
+    return {"median_s": med, "iqr_s": [q1, q3], "cores": cores, "avail": avail, "runs": sum(len(v) for v in results.values()),
+            "runs_at_cores": len(t), "per_thread_setting_us": {str(n): round(statistics.median(v) * 1e6, 1) for n, v in results.items()}}
+
+
+# -- decode workloads -----------------------------------------------------------------------------
+
+
+def run_decode(args: argparse.Namespace, spec: dict) -> dict:
+    import torch
+
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import device_address, pinned_empty
+    from lazykv_amd.quant import packed_pair_bytes
+    from lazykv_amd.workload import draw_layer, to_pool
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    dtype = getattr(torch, spec["dtype"])
+    d, T, L, kind, ks = spec["d"], spec["tokens"], spec["layers"], spec["kind"], spec["k"]
+    N = T // BS
+    n_sealed, fill = N - 1, BS  # lazy sealing: the last block is the current one, full
+    n_cand = n_sealed - 1
+    scale = d**-0.5
+    es = torch.tensor([], dtype=dtype).element_size()
+    P = packed_pair_bytes(BS, d)
+    want_host = kind == "host" and args.only in (None, "zerocopy")
+    want_hbm_leg = kind == "hbm" or (kind == "host" and args.only in (None, "hbm"))
+
+    # ---- state ---------------------------------------------------------------------------------
+    t0 = time.time()
+    layers = []
+    for li in range(L):
+        w = draw_layer(li, N_Q, H, d, T, BS, dtype, device=dev)
+        pool = to_pool(w.keys, w.values, BS)  # [N, h, 2, bs, d] on the GPU
+        kmin = torch.zeros((1, H, N, d), dtype=dtype, device=dev)
+        kmax = torch.zeros_like(kmin)
+        src = kernels.dense_source(w.keys, w.values, BS)
+        st = {"q": w.query.contiguous(), "kmin": kmin, "kmax": kmax, "slots": pool[[0, N - 1]].contiguous(), "needle": w.needle}
+        if kind == "int8":
+            recs = torch.zeros((N, H, P), dtype=torch.uint8, device=dev) if args.tier_where == "hbm" else pinned_empty((N, H, P), torch.uint8)
+            # The records and the metadata of their dequantised keys, in one pass.
+            kernels.store_blocks(src, dst=kernels.record_source(recs, dtype), n_kv=H, head_dim=d, block_size=BS, first_block=0, n_blocks=n_sealed, kmin=kmin, kmax=kmax)
+            st["records"] = recs
+        else:
+            kernels.store_blocks(src, n_kv=H, head_dim=d, block_size=BS, first_block=0, n_blocks=n_sealed, kmin=kmin, kmax=kmax)
+        if kind == "exact":
+            recs = pinned_empty((N, H, P), torch.uint8)
+            kernels.store_blocks(src, dst=kernels.record_source(recs, dtype), n_kv=H, head_dim=d, block_size=BS, first_block=0, n_blocks=n_sealed)
+            st["records"] = recs
+        if want_host:
+            host = pinned_empty(tuple(pool.shape), dtype, coherent=args.coherent)
+            host.copy_(pool)
+            st["host"] = host
+        if want_hbm_leg or kind == "exact":
+            st["pool"] = pool
+        del w, pool, src
+        layers.append(st)
+        if li % 8 == 7:
+            log(f"built {li + 1}/{L} layers ({time.time() - t0:.1f}s)")
+    torch.cuda.synchronize()
+    log(f"state ready in {time.time() - t0:.1f}s: {L} layers x {N} blocks, kind {kind}")
+
+    # ---- legs: (name, k, selected source per layer, remainder source per layer or None) -----------
+    legs = []
+    if kind == "host":
+        if want_host:
+            legs.append(("zerocopy", ks[0], [kernels.pool_source(st["host"]) for st in layers], None))
+        if want_hbm_leg:
+            legs.append(("hbm", ks[0], [kernels.pool_source(st["pool"]) for st in layers], None))
+    elif kind == "hbm":
+        legs.append(("hbm", ks[0], [kernels.pool_source(st["pool"]) for st in layers], None))
+    elif kind == "int8":
+        legs.append((f"int8_{args.tier_where}", ks[0], [kernels.record_source(st["records"], dtype) for st in layers], None))
+    else:
+        for k in ks:
+            legs.append((f"exact_k{k}", k, [kernels.pool_source(st["pool"]) for st in layers], [kernels.record_source(st["records"], dtype) for st in layers]))
+
+    outs = [torch.empty((N_Q, d), dtype=dtype, device=dev) for _ in range(L)]
+    lses = [torch.empty((N_Q,), dtype=torch.float32, device=dev) for _ in range(L)]
+    ws_sel, ws_dec = kernels.Workspace(dev), kernels.Workspace(dev)
+    res = {}
+    for name, k, sels, rems in legs:
+        idx = torch.empty((H, k), dtype=torch.int32, device=dev)
+        ranks, decodes = [], []
+        for li, st in enumerate(layers):
+            ranks.append(kernels.PreparedBoundTopk(st["q"], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx, ws=ws_sel))
+            ss = kernels.pool_source(st["slots"])
+            extra = dict(rem=rems[li], rem_range=(1, n_sealed)) if rems is not None else {}
+            decodes.append(kernels.PreparedDecode(st["q"], n_kv=H, block_size=BS, scale=scale, sel=sels[li], idx=idx, sink=ss, sink_block=0, cur=ss, cur_block=1,
+                                                  fill=fill, out=outs[li], lse=lses[li], ws=ws_dec, **extra))
+
+        def step(ranks=ranks, decodes=decodes) -> None:  # noqa: ANN001
+            for rk, dc in zip(ranks, decodes):
+                rk()
+                dc()
+
+        # Every layer's needle is selected for every KV head; outputs are finite.
+        for li in range(L):
+            ranks[li]()
+            got = idx.cpu()
+            assert (got == layers[li]["needle"]).any(dim=1).all(), f"layer {li}: needle block {layers[li]['needle']} not selected"
+            decodes[li]()
+        torch.cuda.synchronize()
+        assert all(torch.isfinite(o.float()).all() for o in outs), "non-finite output"
+        ms_step, wall = time_step(step, args.steps, args.warmup, args.eager)
+        per = [kernel_us([ranks[li], decodes[li]], max(2, min(5, args.steps))) for li in range(L)]
+        sel_us = statistics.mean(x[0] for x in per)
+        dec_us = statistics.mean(x[1] for x in per)
+        log(f"{name}: {ms_step:.3f} ms/step = {ms_step * 1e3 / L:.1f} us/layer (bound+topk {sel_us:.1f} us, decode {dec_us:.1f} us), wall {wall:.2f}s")
+        res[name] = {"k": k, "ms_step": ms_step, "us_layer": ms_step * 1e3 / L, "sel_us": sel_us, "dec_us": dec_us, "host_sel": bool(sels[0].flags), "rem": rems is not None}
+
+    # ---- probes --------------------------------------------------------------------------------
+    probe = {}
+    host_buf = None
+    for st in layers:
+        if "host" in st:
+            host_buf = st["host"]
+        elif "records" in st and not st["records"].is_cuda:
+            host_buf = st["records"]
+        if host_buf is not None:
+            break
+    if host_buf is not None:
+        probe["pcie_read_gbps"] = probe_gbps(device_address(host_buf), host_buf.numel() * host_buf.element_size() // 16 * 16, 2048)
+    big = torch.empty(4 << 30, dtype=torch.uint8, device=dev)
+    probe["hbm_read_gbps"] = probe_gbps(big.data_ptr(), big.numel(), 4096)
+    del big
+    log(f"probes: {probe}")
+
+    # ---- bytes per layer, roofline -------------------------------------------------------------
+    B_meta = 2 * H * n_cand * d * es
+    B_q = N_Q * d * es
+    B_out = N_Q * d * es + 4 * N_Q
+    B_sinkcur = 2 * H * 2 * BS * d * es
+
+    def leg_bytes(rr: dict) -> tuple[int, int, int, int]:
+        """(selected bytes, remainder bytes, HBM bytes per layer, PCIe bytes per layer)."""
+        k = rr["k"]
+        b_sel = H * k * P if kind == "int8" else 2 * H * k * BS * d * es
+        b_rem = H * (n_cand - k) * P if rr["rem"] else 0
+        hbm = B_meta + 2 * B_q + B_out + B_sinkcur + (0 if rr["host_sel"] else b_sel)
+        pcie = (b_sel if rr["host_sel"] else 0) + b_rem
+        return b_sel, b_rem, hbm, pcie
+
+    legs_out = {}
+    for name, rr in res.items():
+        b_sel, b_rem, hb, pb = leg_bytes(rr)
+        t_roof = max(hb / (HBM_PEAK_GBPS * 1e9), pb / (PCIE_PEAK_GBPS * 1e9)) * 1e6
+        bw_probe = probe.get("pcie_read_gbps")
+        t_probe = max(hb / (HBM_PEAK_GBPS * 1e9), pb / (bw_probe * 1e9)) * 1e6 if (bw_probe and pb) else None
+        dec_pcie = (b_sel if rr["host_sel"] else 0) + b_rem
+        dec_hbm = B_sinkcur + B_q + B_out + (0 if rr["host_sel"] else b_sel)
+        legs_out[name] = {
+            "k": rr["k"], "us_per_layer": round(rr["us_layer"], 3), "ms_per_step": round(rr["ms_step"], 4),
+            "hbm_bytes_per_layer": hb, "pcie_bytes_per_layer": pb,
+            "t_roof_us": round(t_roof, 3), "frac": round(t_roof / rr["us_layer"], 4),
+            "t_roof_us_at_probe": round(t_probe, 2) if t_probe else None, "frac_at_probe": round(t_probe / rr["us_layer"], 4) if t_probe else None,
+            "bound_topk_us": round(rr["sel_us"], 2), "bound_topk_gbps": round((B_meta + B_q) / (rr["sel_us"] * 1e-6) / 1e9, 1),
+            "sparse_decode_us": round(rr["dec_us"], 2), "sparse_decode_pcie_bytes": dec_pcie, "sparse_decode_hbm_bytes": dec_hbm,
+            "sparse_decode_pcie_gbps": round(dec_pcie / (rr["dec_us"] * 1e-6) / 1e9, 2) if dec_pcie else None,
+            "sparse_decode_hbm_gbps": round(dec_hbm / (rr["dec_us"] * 1e-6) / 1e9, 1),
+        }
+
+    main_leg = next(iter(res))
+    m = legs_out[main_leg]
+    names = {
+        "host": f"Llama-3.1-8B-shaped tiered decode step: {L} selecting layers, {T} tokens, 16-token blocks, K={m['k']} of {n_cand} candidates per KV head (6.25% budget), bf16 KV in mapped pinned host memory",
+        "hbm": f"Llama-3.2-1B-shaped decode layer: {T} tokens, d {d}, float16, 16-token blocks, K={m['k']} of {n_cand} candidates per KV head, all in HBM ({L} rotated layer instances)",
+        "int8": f"Llama-3.2-1B-shaped decode step: {L} selecting layers, {T} tokens, d {d}, float16, K={m['k']} of {n_cand} per KV head, sealed blocks as int8 records in {'HBM' if args.tier_where == 'hbm' else 'mapped host memory'}, dequantised on load",
+        "exact": f"Llama-3.1-8B-shaped exact tiered decode step: {L} layers, {T} tokens, bf16, K of {n_cand} from the exact HBM store, every other sealed block from the int8 host tier, merged by LSE",
     }
+    out = {
+        "metric": METRIC if kind == "host" else f"{kind} decode-step µs/layer & achieved GB/s (% byte roofline)",
+        "value": m["us_per_layer"],
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": m["ms_per_step"],
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == torch.bfloat16 else "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": names[kind],
+            "layers": L, "tokens": T, "q_heads": N_Q, "kv_heads": H, "head_dim": d, "block_size": BS, "k": m["k"],
+            "rank_dtype": "float32", "dense_layers": 0, "launch": "eager" if args.eager else "hip_graph",
+            "host_memory": "fine-grained" if args.coherent else "coarse-grained",
+        },
+        "host_syncs_per_layer": 0,
+    }
+    # The dominant kernel is lkv_sparse_decode (sparse_decode_kernel + decode_merge_kernel).
+    traffic = pmc_traffic() if kind == "host" else {}
+    if m["sparse_decode_pcie_bytes"]:
+        gbps = m["sparse_decode_pcie_gbps"]
+        out["roofline"] = {"bound": "pcie", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, host reads over PCIe", "achieved": gbps,
+                           "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get("zerocopy/sparse_decode_kernel"),
+                           "algorithmic_bytes": m["sparse_decode_pcie_bytes"], "kernel_us": m["sparse_decode_us"]}
+        if traffic:
+            out["roofline"]["traffic_note"] = ("calibrated FETCH_SIZE + WRITE_SIZE bytes per launch, host (PCIe) and HBM fetches together; algorithmic total incl. HBM part "
+                                               f"{m['sparse_decode_pcie_bytes'] + m['sparse_decode_hbm_bytes']}; source {TRAFFIC_FILE.relative_to(ROOT)}")
+    else:
+        gbps = m["sparse_decode_hbm_gbps"]
+        out["roofline"] = {"bound": "hbm", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, HBM", "achieved": gbps,
+                           "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get("hbm/sparse_decode_kernel"),
+                           "algorithmic_bytes": m["sparse_decode_hbm_bytes"], "kernel_us": m["sparse_decode_us"]}
+    out["byte_roofline"] = {"hbm_bytes_per_layer": m["hbm_bytes_per_layer"], "pcie_bytes_per_layer": m["pcie_bytes_per_layer"],
+                            "t_roof_us_at_64gbps": m["t_roof_us"], "frac_at_64gbps": m["frac"],
+                            "t_roof_us_at_probe": m["t_roof_us_at_probe"], "frac_at_probe": m["frac_at_probe"]}
+    out["kernels"] = {"bound_topk": {"us": m["bound_topk_us"], "hbm_bytes": B_meta + B_q, "gbps": m["bound_topk_gbps"],
+                                     "frac_hbm_peak": round(m["bound_topk_gbps"] / HBM_PEAK_GBPS, 4)},
+                      "sparse_decode": {"us": m["sparse_decode_us"], "pcie_bytes": m["sparse_decode_pcie_bytes"], "hbm_bytes": m["sparse_decode_hbm_bytes"],
+                                        "pcie_gbps": m["sparse_decode_pcie_gbps"], "hbm_gbps": m["sparse_decode_hbm_gbps"]}}
+    if kind == "host" and "hbm" in legs_out:
+        hb = legs_out["hbm"]
+        out["hbm_resident"] = {"us_per_layer": hb["us_per_layer"], "ms_per_step": hb["ms_per_step"], "hbm_bytes_per_layer": hb["hbm_bytes_per_layer"],
+                               "t_roof_us": hb["t_roof_us"], "frac": hb["frac"], "bound_topk_us": hb["bound_topk_us"], "bound_topk_gbps": hb["bound_topk_gbps"],
+                               "sparse_decode_us": hb["sparse_decode_us"], "sparse_decode_gbps": hb["sparse_decode_hbm_gbps"]}
+        if main_leg == "hbm":
+            out["config"]["workload"] = out["config"]["workload"].replace("bf16 KV in mapped pinned host memory", "bf16 KV resident in HBM")
+    if len(legs_out) > 1 and kind != "host":
+        out["legs"] = legs_out
+    out["probes"] = {kk: round(v, 2) for kk, v in probe.items()}
+
+    # ---- CPU baseline: the reference's path for this workload on this host's cores ---------------
+    if not args.no_cpu_baseline:
+        last = list(res.values())[-1]
+        out["cpu_baseline"] = cpu_baseline_decode(kind, layers, ks[0], n_sealed, fill, scale, args.cpu_seconds, outs, last)
+    return out
+
+
+def cpu_baseline_decode(kind: str, layers: list, k: int, n_sealed: int, fill: int, scale: float, budget_s: float, outs: list, last_leg: dict) -> dict:
+    from oracle import cpu_path
+
+    n_layers = min(len(layers), 2 if kind == "exact" else 8)
+    states, fn = [], None
+    for st in layers[:n_layers]:
+        sink, cur = st["slots"][0].cpu(), st["slots"][1].cpu()
+        q, kmin, kmax = st["q"].cpu(), st["kmin"].cpu(), st["kmax"].cpu()
+        if kind == "host":
+            fn = cpu_path.decode_layer
+            states.append((q, kmin, kmax, n_sealed, k, st["host"], sink, cur, fill, scale))
+        elif kind == "hbm":
+            fn = cpu_path.decode_layer
+            states.append((q, kmin, kmax, n_sealed, k, st["pool"].cpu(), sink, cur, fill, scale))
+        elif kind == "int8":
+            fn = cpu_path.decode_layer_int8
+            states.append((q, kmin, kmax, n_sealed, k, st["records"].cpu(), sink, cur, fill, scale))
+        else:
+            fn = cpu_path.exact_layer
+            pool = st["pool"].cpu()
+            hh, bs, d = pool.shape[1], pool.shape[3], pool.shape[-1]
+            mk = pool[:n_sealed, :, 0].permute(1, 0, 2, 3).reshape(hh, n_sealed * bs, d).float().contiguous()
+            mv = pool[:n_sealed, :, 1].permute(1, 0, 2, 3).reshape(hh, n_sealed * bs, d).float().contiguous()
+            states.append((q, kmin, kmax, n_sealed, k, pool, mk, mv, cur, fill, scale))
+    # Sanity beside the timing: the CPU path's layer-0 output against the GPU's (last leg run).
+    r0 = fn(*states[0])
+    diff = float((r0[0] - outs[0].float().cpu()).abs().max()) if last_leg["k"] == k else None
+    t = time_cpu(fn, states, budget_s)
+    samples = {"host": "single-layer decodes: fp32 quest bound, topk, index_select gather from the host pool, cat, masked fp32 attention + logsumexp",
+               "hbm": "single-layer decodes: fp32 quest bound, topk, index_select gather, cat, masked fp32 attention + logsumexp",
+               "int8": "single-layer decodes: fp32 quest bound, topk, gather of int8 records, quant.py unpack, cat, masked fp32 attention + logsumexp",
+               "exact": f"single-layer exact decodes at K={k}: the gathered partial as in decode, the batched masked CPU partial over the float32 mirror of every sealed block, LSE merge"}
+    return {
+        "value": round(t["median_s"] * 1e6, 1), "unit": "us/layer", "cores": t["cores"], "kind": "port",
+        "sample": f"{t['runs']} {samples[kind]} (layers 0-{n_layers - 1} of the same workload; median over {t['runs_at_cores']} at {t['cores']} threads), torch CPU ops in the reference's order",
+        "iqr_us": [round(x * 1e6, 1) for x in t["iqr_s"]], "per_thread_setting_us": t["per_thread_setting_us"],
+        "cpu_model": cpu_model(), "host_cpus_visible": t["avail"], "gpu_vs_cpu_layer0_max_abs_out": diff,
+    }
+
+
+# -- layer-major prefill into the int8 host tier ------------------------------------------------------
+
+
+def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from lazykv_amd.attention import IMPLEMENTATION_NAME, install
+    from lazykv_amd.cache import FullGPUCache
+    from lazykv_amd.quant import packed_pair_bytes
+    from lazykv_amd.tiered import TieredCache, allocate_host_pools
+    from lazykv_amd.tiered_prefill import tiered_prefill
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    n, L, d, k = spec["tokens"], spec["layers"], spec["d"], spec["k"][0]
+    chunk = 4096
+    reps = max(1, min(args.steps, 5))
+    install()
+    cfg = LlamaConfig(hidden_size=2048, intermediate_size=8192, num_hidden_layers=L, num_attention_heads=N_Q, num_key_value_heads=H, head_dim=d,
+                      vocab_size=128256, max_position_embeddings=131072, rope_theta=500000.0, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    t0 = time.time()
+    with torch.device(dev):
+        model = LlamaForCausalLM(cfg)  # Linear and embedding weights ~ N(0, 0.02), RMSNorm gains 1
+    model.set_attn_implementation(IMPLEMENTATION_NAME)
+    model = model.to(dtype=torch.float16).eval()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    ids = torch.randint(0, cfg.vocab_size, (1, n), device=dev, generator=gen)
+    cap = n + 64
+    pools = allocate_host_pools(L, H, d, BS, cap, torch.float16, quant="int8")
+    log(f"model and pools ready in {time.time() - t0:.1f}s")
+    runs = []
+    for i in range(args.warmup + reps):
+        r = tiered_prefill(model, ids, chunk, k, BS, cap, dense_layers=0, host_pools=pools, quant="int8")
+        if i >= args.warmup:
+            runs.append((r.wall_s, r.boundary_layer_s, r.chunks))
+        del r
+    boundary_us = statistics.mean(statistics.mean(b) for _, b, _ in runs) * 1e6
+    wall_s = statistics.median(w for w, _, _ in runs)
+    # The path it replaces: chunk-major prefill into a full cache, then the tiers built from it.
+    ref_walls = []
+    for i in range(args.warmup + reps):
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        with torch.inference_mode():
+            full = FullGPUCache(L, cap)
+            for s in range(0, n, chunk):
+                model(input_ids=ids[:, s : s + chunk], past_key_values=full, use_cache=True, logits_to_keep=1)
+            cache = TieredCache(full, k, BS, cap, dense_layers=0, host_pools=pools, quant="int8")
+        torch.cuda.synchronize()
+        if i >= args.warmup:
+            ref_walls.append(time.perf_counter() - w0)
+        del full, cache
+    ref_wall = statistics.median(ref_walls)
+    nb = n // BS
+    P = packed_pair_bytes(BS, d)
+    b_read = 2 * H * nb * BS * d * 2  # the layer's float16 K and V
+    b_rec = nb * H * P  # int8 records, written to mapped host memory
+    b_meta = 2 * H * nb * d * 2
+    pcie = b_rec / (boundary_us * 1e-6) / 1e9
+    t_roof = max((b_read + b_meta) / (HBM_PEAK_GBPS * 1e9), b_rec / (PCIE_PEAK_GBPS * 1e9)) * 1e6
+    log(f"prefill32k: tier build {boundary_us:.1f} us/layer ({pcie:.1f} GB/s of records to host), prefill wall {wall_s:.3f}s vs chunk-major + tier build {ref_wall:.3f}s")
+    out = {
+        "metric": "tiered prefill: int8 tier build µs/layer (fused pack + key min/max, records written to mapped host memory) & achieved PCIe GB/s (% roofline)",
+        "value": round(boundary_us, 2), "unit": "us/layer", "n_gpus": 1, "steps": reps, "warmup": args.warmup,
+        "ms_per_step": round(boundary_us * L / 1e3, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": f"Llama-3.2-1B-shaped layer-major prefill: {L} layers (hidden 2048, 32/8 heads, d {d}), {n}-token prompt uniform over 128,256 ids, "
+                               f"float16 weights ~N(0,0.02), chunks of {chunk}, every layer's KV into the int8 host tier (dense_layers 0)",
+                   "layers": L, "tokens": n, "q_heads": N_Q, "kv_heads": H, "head_dim": d, "block_size": BS, "k": k, "chunk": chunk, "dense_layers": 0},
+        "roofline": {"bound": "pcie", "kernel": "store_blocks_kernel (int8 records to host + metadata of the dequantised keys)", "achieved": round(pcie, 2),
+                     "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(pcie / PCIE_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes": b_rec, "kernel_us": round(boundary_us, 2),
+                     "hbm_read_bytes": b_read, "hbm_read_gbps": round(b_read / (boundary_us * 1e-6) / 1e9, 1), "metadata_bytes": b_meta},
+        "byte_roofline": {"hbm_bytes_per_layer": b_read + b_meta, "pcie_bytes_per_layer": b_rec, "t_roof_us_at_64gbps": round(t_roof, 2),
+                          "frac_at_64gbps": round(t_roof / boundary_us, 4)},
+        "prefill": {"wall_s": round(wall_s, 4), "per_layer_ms": round(wall_s / L * 1e3, 3), "chunks": runs[0][2],
+                    "chunk_major_then_tier_wall_s": round(ref_wall, 4), "ratio_to_chunk_major": round(wall_s / ref_wall, 4)},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import cpu_path
+
+        with torch.inference_mode():
+            full = FullGPUCache(L, cap)
+            for s in range(0, n, chunk):
+                model(input_ids=ids[:, s : s + chunk], past_key_values=full, use_cache=True, logits_to_keep=1)
+        states = [(full.layers[i].keys[0, :, :n].cpu(), full.layers[i].values[0, :, :n].cpu(), BS) for i in range(min(2, L))]
+        del full
+        t = time_cpu(cpu_path.tier_build_layer, states, args.cpu_seconds)
+        out["cpu_baseline"] = {
+            "value": round(t["median_s"] * 1e6, 1), "unit": "us/layer", "cores": t["cores"], "kind": "port",
+            "sample": f"{t['runs']} single-layer int8 tier builds of the same prefill's KV (layers 0-{len(states) - 1}): quant.py pack, unpack, key min/max in torch CPU ops "
+                      f"(median over {t['runs_at_cores']} at {t['cores']} threads)",
+            "iqr_us": [round(x * 1e6, 1) for x in t["iqr_s"]], "per_thread_setting_us": t["per_thread_setting_us"],
+            "cpu_model": cpu_model(), "host_cpus_visible": t["avail"],
+        }
+    return out
 
 
 if __name__ == "__main__":
