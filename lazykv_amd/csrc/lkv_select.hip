@@ -40,7 +40,6 @@ constexpr int kBlocksPerWG = kBoundWaves * 4 * kIter;     // candidate blocks pe
 constexpr int kSelThreads = 512;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kBins = 2048;
-constexpr int kScanWords = 64;
 constexpr int kPerThread = 24;                            // candidate keys held per thread
 constexpr int kMaxCand = kSelThreads * kPerThread;        // 12288 candidates per KV head
 constexpr int kMaxSortedK = 2048;
@@ -123,9 +122,9 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
   }
 }
 
-// Exclusive prefix sum over the workgroup's threads (ascending thread id); *total gets the sum.
-// Uses scan[0..kSelWaves).
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* scan, uint32_t* total) {
+// Exclusive prefix sum over the workgroup's threads (ascending thread id). `slots` holds one word
+// per wave and is read after a barrier; the caller separates reuses of `slots` by a barrier.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* slots, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint32_t x = v;
 #pragma unroll
@@ -133,31 +132,42 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s
     uint32_t y = __shfl_up(x, o, 64);
     if (lane >= o) x += y;
   }
-  if (lane == 63) scan[wave] = x;
+  if (lane == 63) slots[wave] = x;
   __syncthreads();
   uint32_t before = 0, all = 0;
 #pragma unroll
   for (int w = 0; w < kSelWaves; ++w) {
-    uint32_t s = scan[w];
+    uint32_t s = slots[w];
     if (w < wave) before += s;
     all += s;
   }
-  __syncthreads();
   *total = all;
   return before + x - v;
 }
 
+constexpr int kStage = 4096;  // ids staged in LDS per coalesced write-out round
+
 __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __restrict__ bounds, int64_t bstride,
                                                              int n_cand, int k, int cand_offset, int sorted,
                                                              int32_t* __restrict__ out_idx, int64_t idx_stride) {
-  // Region reused in turn: histogram (kBins), then the boundary-bin list (2 * kSelThreads) and its
-  // taken bitmap, then the 64-bit sort slots (2 * kp2 <= 2 * kMaxSortedK words).
-  constexpr int kRegion = 2 * kMaxSortedK > kBins ? 2 * kMaxSortedK : kBins;
-  static_assert(2 * kSelThreads + (kMaxCand + 31) / 32 <= kRegion, "list and bitmap must fit the region");
-  __shared__ __align__(16) uint32_t region[kRegion];
-  __shared__ uint32_t scan[kScanWords];
+  // LDS, one region per use so that phases need no barrier before reusing memory:
+  //   hist      -- radix histogram (kBins)
+  //   list      -- the boundary bin's keys and ids (2 * kSelThreads)
+  //   taken     -- bitmap of the boundary-bin keys that rank among the best (one bit per candidate)
+  //   stage     -- the selected ids in output order, written out coalesced (kStage), or the
+  //                64-bit sort slots of the sorted mode (2 * kp2 <= 2 * kMaxSortedK words)
+  //   mm / scan_* / info -- per-wave partials and broadcast words
+  static_assert(2 * kMaxSortedK <= kStage, "sort slots must fit the staging region");
+  __shared__ uint32_t hist[kBins + 64];  // + one spare bin per lane for keys outside the range
+  __shared__ uint32_t list[2 * kSelThreads];
+  __shared__ uint32_t taken[(kMaxCand + 31) / 32];
+  __shared__ __align__(16) uint32_t stage[kStage + 64];  // + one spare slot per lane
+  __shared__ uint32_t mm[2 * kSelWaves];
+  __shared__ uint32_t scan_pass[kSelWaves], scan_out[kSelWaves];
+  __shared__ uint32_t info[4];  // boundary bin, keys above it, keys in it, boundary-list length
   const int h = blockIdx.x;
   const int n = n_cand;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // Keys per thread, a multiple of 4 so a thread's run is whole 16-byte vectors when rows are
   // padded (bstride % 4 == 0).
   const int npt = ((n + kSelThreads - 1) / kSelThreads + 3) & ~3;
@@ -180,45 +190,39 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) key[u] = (u < npt && i0 + u < n) ? orderable(bound_h[i0 + u]) : 0u;
   }
-  bool live[kPerThread];
+  // While the loads are in flight: clear the bitmap (read only after two later barriers).
+  for (int i = threadIdx.x; i < (kMaxCand + 31) / 32; i += kSelThreads) taken[i] = 0u;
+  // Slots u < nlive hold candidates (a count, not a per-slot flag array: an array of divergent
+  // booleans lives in scalar register pairs and spills).
+  const int nlive = max(0, min(npt, n - i0));
   uint32_t lmin = 0xffffffffu, lmax = 0u;
 #pragma unroll
   for (int u = 0; u < kPerThread; ++u) {
-    live[u] = u < npt && i0 + u < n;
-    if (live[u]) {
-      lmin = min(lmin, key[u]);
-      lmax = max(lmax, key[u]);
-    }
+    lmin = min(lmin, u < nlive ? key[u] : 0xffffffffu);
+    lmax = max(lmax, u < nlive ? key[u] : 0u);
   }
   // Workgroup min and max in one reduction.
-  {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      lmin = min(lmin, (uint32_t)__shfl_xor(lmin, o, 64));
-      lmax = max(lmax, (uint32_t)__shfl_xor(lmax, o, 64));
-    }
-    if (lane == 0) {
-      scan[2 * wave] = lmin;
-      scan[2 * wave + 1] = lmax;
-    }
-    __syncthreads();
-    lmin = scan[0];
-    lmax = scan[1];
-#pragma unroll
-    for (int w = 1; w < kSelWaves; ++w) {
-      lmin = min(lmin, scan[2 * w]);
-      lmax = max(lmax, scan[2 * w + 1]);
-    }
-    __syncthreads();
+  for (int o = 32; o > 0; o >>= 1) {
+    lmin = min(lmin, (uint32_t)__shfl_xor(lmin, o, 64));
+    lmax = max(lmax, (uint32_t)__shfl_xor(lmax, o, 64));
   }
-  uint32_t lo = lmin, hi = lmax;
+  if (lane == 0) {
+    mm[2 * wave] = lmin;
+    mm[2 * wave + 1] = lmax;
+  }
+  __syncthreads();
+  uint32_t lo = mm[0], hi = mm[1];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    lo = min(lo, mm[2 * w]);
+    hi = max(hi, mm[2 * w + 1]);
+  }
 
   // ---- range-adaptive radix select of the k-th largest key --------------------------------------
   int need = k;  // keys still to take from [lo, hi]; every key above hi is taken
   uint32_t T;    // after the loop: take every key > T, `need` keys == T, and the marked keys
   uint32_t marked = 0u;  // bit u: key[u] lies in the final bin and ranks among the `need` best
-  uint32_t* hist = region;
 #pragma unroll 1
   while (true) {
     if (lo >= hi) {
@@ -231,9 +235,11 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
     const int nb = (int)(width >> shift) + 1;  // at most 2048 bins
     for (int i = threadIdx.x; i < nb; i += kSelThreads) hist[i] = 0;
     __syncthreads();
+    // Branch-free: a key outside the range (or an empty slot) counts in this lane's spare bin.
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
-      if (live[u] && key[u] >= lo && key[u] <= hi) atomicAdd(&hist[(key[u] - lo) >> shift], 1u);
+      const bool in = u < nlive && key[u] >= lo && key[u] <= hi;
+      atomicAdd(&hist[in ? (key[u] - lo) >> shift : kBins + lane], 1u);
     }
     __syncthreads();
     // Thread t owns bins [t*per, (t+1)*per); the bins above it hold `above` keys.
@@ -244,7 +250,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
       if (bin < nb) local += hist[bin];
     }
     uint32_t total;
-    const uint32_t below = block_exclusive_scan(local, scan, &total);
+    const uint32_t below = block_exclusive_scan(local, scan_pass, &total);
     const uint32_t above = total - below - local;
     if (above < (uint32_t)need && (uint32_t)need <= above + local) {
       uint32_t acc = above;
@@ -252,52 +258,45 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
         const int bin = threadIdx.x * per + j;
         const uint32_t cnt = bin < nb ? hist[bin] : 0u;
         if ((uint32_t)need <= acc + cnt) {
-          scan[kSelWaves] = (uint32_t)bin;
-          scan[kSelWaves + 1] = acc;
-          scan[kSelWaves + 2] = cnt;
+          info[0] = (uint32_t)bin;
+          info[1] = acc;
+          info[2] = cnt;
+          info[3] = 0u;
           break;
         }
         acc += cnt;
       }
     }
     __syncthreads();
-    const uint32_t bin = scan[kSelWaves];
-    need -= (int)scan[kSelWaves + 1];
-    const uint32_t in_bin = scan[kSelWaves + 2];
+    const uint32_t bin = info[0];
+    need -= (int)info[1];
+    const uint32_t in_bin = info[2];
     const uint32_t new_lo = lo + (bin << shift);
     const uint32_t span = shift ? ((1u << shift) - 1u) : 0u;
     hi = min(hi, new_lo + span);
     lo = new_lo;
-    __syncthreads();
     if (lo < hi && in_bin <= (uint32_t)kSelThreads) {
       // Few keys left in the bin: rank them directly instead of more passes. They are listed (in
       // any order) and ranked by (key desc, id asc); the `need` best are marked in a bitmap that
       // each thread reads back for its own run of candidates.
-      uint32_t* list_key = region;
-      uint32_t* list_id = region + kSelThreads;
-      if (threadIdx.x == 0) scan[kSelWaves + 3] = 0;
-      __syncthreads();
+      uint32_t* list_key = list;
+      uint32_t* list_id = list + kSelThreads;
 #pragma unroll
       for (int u = 0; u < kPerThread; ++u) {
-        if (live[u] && key[u] >= lo && key[u] <= hi) {
-          const uint32_t slot = atomicAdd(&scan[kSelWaves + 3], 1u);
+        if (u < nlive && key[u] >= lo && key[u] <= hi) {
+          const uint32_t slot = atomicAdd(&info[3], 1u);
           list_key[slot] = key[u];
           list_id[slot] = (uint32_t)(i0 + u);
         }
       }
       __syncthreads();
-      const int m = (int)scan[kSelWaves + 3];
-      // Thread e ranks list entry e and marks it, by index, when it is among the `need` best.
-      uint32_t* taken = region + 2 * kSelThreads;  // one bit per candidate
-      for (int i = threadIdx.x; i < (kMaxCand + 31) / 32; i += kSelThreads) taken[i] = 0u;
-      __syncthreads();
+      const int m = (int)info[3];
       if ((int)threadIdx.x < m) {
         const uint32_t mk = list_key[threadIdx.x], mi = list_id[threadIdx.x];
         int rank = 0;
-#pragma unroll 8
         for (int e = 0; e < m; ++e) {
-          const uint32_t ek = list_key[e];
-          rank += ek > mk || (ek == mk && list_id[e] < mi);
+          const uint32_t ek = list_key[e], ei = list_id[e];
+          rank += (ek > mk) | ((ek == mk) & (ei < mi));
         }
         if (rank < need) atomicOr(&taken[mi >> 5], 1u << (mi & 31));
       }
@@ -311,53 +310,65 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
       need = 0;
       break;
     }
+    __syncthreads();  // info and hist are rewritten by the next pass
   }
 
   // ---- ordered compaction: ascending block id ----------------------------------------------------
   // One scan of (ties, taken-above) counts; ties are taken in index order, so the ties before a
   // thread that are taken number min(ties before, need).
-  uint32_t gt = 0, eq = 0;
+  // Per thread, two bit masks over its slots: keys taken outright (above T, or marked) and ties
+  // (== T, unmarked). Built branch-free, kept in vector registers.
+  uint32_t above_m = 0u, tie_m = 0u;
 #pragma unroll
   for (int u = 0; u < kPerThread; ++u) {
-    if (live[u]) {
-      const bool m = (marked >> u) & 1u;
-      gt += key[u] > T || m;
-      eq += key[u] == T && !m;
-    }
+    const uint32_t mk = (marked >> u) & 1u;
+    const uint32_t lv = u < nlive ? 1u : 0u;
+    above_m |= (lv & ((key[u] > T ? 1u : 0u) | mk)) << u;
+    tie_m |= (lv & (key[u] == T ? 1u : 0u) & (mk ^ 1u)) << u;
   }
+  const uint32_t gt = __popc(above_m), eq = __popc(tie_m);
   uint32_t tot;
-  const uint32_t packed = block_exclusive_scan((eq << 16) | gt, scan, &tot);
+  const uint32_t packed = block_exclusive_scan((eq << 16) | gt, scan_out, &tot);
   const int eq_before = (int)(packed >> 16), gt_before = (int)(packed & 0xffffu);
   int take_eq = need - eq_before;
   take_eq = take_eq < 0 ? 0 : (take_eq > (int)eq ? (int)eq : take_eq);
-  uint32_t pos = (uint32_t)gt_before + (uint32_t)min(eq_before, need);
-  uint64_t* sortbuf = reinterpret_cast<uint64_t*>(region);  // free after the passes
+  const uint32_t pos0 = (uint32_t)gt_before + (uint32_t)min(eq_before, need);
+  // Ties are taken in index order: this thread's first take_eq ties.
+  uint32_t ties_taken = tie_m;
+  for (int t = (int)eq; t > take_eq; --t) ties_taken &= ~(0x80000000u >> __clz(ties_taken));  // drop the highest
+  const uint32_t tk = above_m | ties_taken;  // the slots this thread contributes, in index order
   int32_t* out_h = out_idx + (int64_t)h * idx_stride;
-  int taken_eq = 0;
+  if (!sorted) {
+    // The ids go to LDS at their output positions, then out in coalesced rounds of kStage.
+    for (int base = 0; base < k; base += kStage) {
+      const uint32_t lim = (uint32_t)min(base + kStage, k);
+      uint32_t pos = pos0;
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) {
-    if (live[u]) {
-      const int i = i0 + u;
-      bool take = key[u] > T || ((marked >> u) & 1u);
-      if (!take && key[u] == T && taken_eq < take_eq) {
-        take = true;
-        ++taken_eq;
+      for (int u = 0; u < kPerThread; ++u) {
+        const uint32_t bit = (tk >> u) & 1u;
+        const bool here = bit && pos >= (uint32_t)base && pos < lim;
+        stage[here ? pos - base : kStage + lane] = (uint32_t)(i0 + u);  // branch-free: spare slot otherwise
+        pos += bit;
       }
-      if (take) {
-        if (pos < (uint32_t)k) {  // exactly k are taken; the guard keeps a logic error in bounds
-          if (sorted) {
-            sortbuf[pos] = ((uint64_t)key[u] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-          } else {
-            out_h[pos] = i + cand_offset;
-          }
-        }
+      __syncthreads();
+      for (int i = threadIdx.x; i < kStage && base + i < k; i += kSelThreads) out_h[base + i] = (int32_t)stage[i] + cand_offset;
+      __syncthreads();
+    }
+    return;
+  }
+
+  // ---- sorted mode: bitonic sort, descending (key, then lower id first) --------------------------
+  uint64_t* sortbuf = reinterpret_cast<uint64_t*>(stage);
+  {
+    uint32_t pos = pos0;
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) {
+      if ((tk >> u) & 1u) {
+        if (pos < (uint32_t)k) sortbuf[pos] = ((uint64_t)key[u] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i0 + u));
         ++pos;
       }
     }
   }
-  if (!sorted) return;
-
-  // ---- bitonic sort, descending (key, then lower id first) ---------------------------------------
   int kp2 = 1;
   while (kp2 < k) kp2 <<= 1;
   for (int i = k + threadIdx.x; i < kp2; i += kSelThreads) sortbuf[i] = 0;
