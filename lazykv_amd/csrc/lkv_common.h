@@ -50,6 +50,25 @@ static inline bool lkv_is_model_dtype(int dt) { return dt == LKV_F16 || dt == LK
 
 static inline int lkv_dtype_size(int dt) { return dt == LKV_F32 ? 4 : (dt == LKV_INT8_RECORD ? 1 : 2); }
 
+// Host-memory traffic a launch keeps in flight, in bytes. Mapped host memory is served over PCIe
+// faster from a shallow queue than from a deep one, and the best depth depends on the access
+// pattern (measured on MI355X at the workload shapes):
+//   reads of scattered pairs (a selected set): ~2 MiB. 8 KiB bf16 pairs read at 56.1 GB/s with
+//     2 MiB in flight, 53.2 GB/s with 8 MiB, 51.7 GB/s with every resident wave's pair (~29 MiB);
+//   reads of runs of consecutive blocks (the exact tier's remainder): ~8 MiB. int8 records read at
+//     55.3 GB/s with 8 MiB, 52.5 GB/s with 2 MiB;
+//   writes (the tier build, seals): ~4 MiB. int8 records written at 52.7 GB/s, 52.1 unbounded.
+// Launches whose blocks live in host memory size their grids from these budgets.
+static inline double lkv_host_read_inflight() { return 2.0 * 1024 * 1024; }
+static inline double lkv_host_stream_inflight() { return 8.0 * 1024 * 1024; }
+static inline double lkv_host_write_inflight() { return 4.0 * 1024 * 1024; }
+
+// Bytes of one (block, head) pair in a source or destination.
+static inline size_t lkv_pair_bytes(const lkv_kv_source* s, int bs, int d) {
+  if (s->dtype == LKV_INT8_RECORD) return (size_t)(2 * bs * d + 4 * d + 4 * bs);
+  return (size_t)2 * bs * d * lkv_dtype_size(s->dtype);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Device side.
 // ---------------------------------------------------------------------------------------------

@@ -527,21 +527,14 @@ struct PlanHints {
   size_t sel_pair = 0, rem_pair = 0;
 };
 
-// Host-memory reads a launch keeps in flight. Reading mapped host memory, the link delivers
-// ~56 GB/s when about 2 MiB of reads are outstanding (64 workgroups of 4 waves, one 8 KiB pair
-// per wave) and ~51 GB/s when every resident wave has its pair outstanding (~29 MiB): a deep
-// queue of reads is served more slowly, so host segments are split into fewer, longer runs.
-constexpr double kHostInflight = 2.0 * 1024 * 1024;
-
-static int host_splits(size_t pair_bytes, int n_kv, double share) {
-  const double wgs = share * kHostInflight / ((double)kWaves * (double)pair_bytes);
+// Host segments are split into fewer, longer runs than HBM ones: enough workgroups that one pair
+// per wave keeps the host read budget in flight, and no more -- lkv_host_read_inflight for the
+// scattered selected pairs, lkv_host_stream_inflight for the remainder's runs of consecutive
+// blocks. For the 8 KiB pairs of a bf16 d128 pool that is 64 workgroups, against 464 for HBM.
+static int host_splits(size_t pair_bytes, int n_kv, double budget) {
+  const double wgs = budget / ((double)kWaves * (double)pair_bytes);
   const int per_head = (int)(wgs / n_kv);
   return per_head < 1 ? 1 : per_head;
-}
-
-static size_t pair_bytes(const lkv_kv_source* s, int bs, int d) {
-  if (s->dtype == LKV_INT8_RECORD) return (size_t)(2 * bs * d + 4 * d + 4 * bs);
-  return (size_t)2 * bs * d * lkv_dtype_size(s->dtype);
 }
 
 // Items per workgroup: about two pairs per wave for the gathered set (enough loads in flight to
@@ -563,16 +556,15 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
   if (p.per_b > 2048) p.per_b = 2048;  // the exclusion bitmap holds 2048 blocks
   p.splits_b = n_b > 0 ? (n_b + p.per_b - 1) / p.per_b : 0;
   const int n_sel = d->attend_selected ? d->k : 0;
-  const double host_items = (hint.sel_host ? n_sel : 0) + (hint.rem_host ? n_b : 0);
   if (hint.sel_host && n_sel > 0) {
-    const int s = host_splits(hint.sel_pair, d->n_kv, n_sel / host_items);
+    const int s = host_splits(hint.sel_pair, d->n_kv, lkv_host_read_inflight());
     if (s < p.splits_a) {
       p.per_a = (p.n_a + s - 1) / s;
       p.splits_a = (p.n_a + p.per_a - 1) / p.per_a;
     }
   }
   if (hint.rem_host && n_b > 0) {
-    int s = host_splits(hint.rem_pair, d->n_kv, n_b / host_items);
+    int s = host_splits(hint.rem_pair, d->n_kv, lkv_host_stream_inflight());
     if (s < (n_b + 2047) / 2048) s = (n_b + 2047) / 2048;  // keeps per_b within the bitmap
     if (s < p.splits_b) {
       p.per_b = (n_b + s - 1) / s;
@@ -693,11 +685,11 @@ extern "C" int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, 
   PlanHints hint;
   if (attend_sel) {
     hint.sel_host = (sel->flags & LKV_SRC_HOST) != 0;
-    hint.sel_pair = pair_bytes(sel, d.block_size, d.head_dim);
+    hint.sel_pair = lkv_pair_bytes(sel, d.block_size, d.head_dim);
   }
   if (has_rem) {
     hint.rem_host = (rem->flags & LKV_SRC_HOST) != 0;
-    hint.rem_pair = pair_bytes(rem, d.block_size, d.head_dim);
+    hint.rem_pair = lkv_pair_bytes(rem, d.block_size, d.head_dim);
   }
   const Plan p = make_plan(desc, hint);
   const int S = p.splits_a + p.splits_b;

@@ -106,13 +106,11 @@ __device__ __forceinline__ void write_meta(const StoreArgs& a, int b, int h, int
 }
 
 template <int D, int MT, int MODE>
-__global__ __launch_bounds__(kThreads) void store_blocks_kernel(StoreArgs a) {
+__device__ __forceinline__ void store_pair(const StoreArgs& a, int64_t pair) {
   using T = typename lkv::Elem<MT>::T;
   constexpr int EPL = D / 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int r = lane >> 4, c = lane & 15;
-  const int64_t pair = (int64_t)blockIdx.x * kWaves + wave;
-  if (pair >= (int64_t)a.n_blocks * a.n_kv) return;  // wave-uniform
   const int b = a.first_block + (int)(pair / a.n_kv);
   const int h = (int)(pair % a.n_kv);
   const int bs = a.bs;
@@ -256,6 +254,15 @@ __global__ __launch_bounds__(kThreads) void store_blocks_kernel(StoreArgs a) {
   }
 }
 
+// One wave per (block, head) pair, the grid striding over the pairs. Waves never synchronise with
+// each other, so a grid smaller than the pair count (a host destination) is just a longer loop.
+template <int D, int MT, int MODE>
+__global__ __launch_bounds__(kThreads) void store_blocks_kernel(StoreArgs a) {
+  const int64_t total = (int64_t)a.n_blocks * a.n_kv;
+  for (int64_t pair = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); pair < total; pair += (int64_t)gridDim.x * kWaves)
+    store_pair<D, MT, MODE>(a, pair);  // `pair` is wave-uniform
+}
+
 // quant.py unpack: records [m, P] -> pairs [m, 2, bs, D] in the model dtype.
 template <int D, int MT>
 __global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t* __restrict__ records, int64_t m, int bs,
@@ -296,9 +303,11 @@ __global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t* __restr
 }
 
 template <int D, int MT>
-int launch_store(hipStream_t s, int mode, const StoreArgs& a) {
+int launch_store(hipStream_t s, int mode, const StoreArgs& a, int64_t max_wgs) {
   const int64_t pairs = (int64_t)a.n_blocks * a.n_kv;
-  const dim3 grid((unsigned)((pairs + kWaves - 1) / kWaves));
+  int64_t wgs = (pairs + kWaves - 1) / kWaves;
+  if (wgs > max_wgs) wgs = max_wgs;
+  const dim3 grid((unsigned)wgs);
   switch (mode) {
     case MODE_META: hipLaunchKernelGGL((store_blocks_kernel<D, MT, MODE_META>), grid, dim3(kThreads), 0, s, a); break;
     case MODE_COPY: hipLaunchKernelGGL((store_blocks_kernel<D, MT, MODE_COPY>), grid, dim3(kThreads), 0, s, a); break;
@@ -312,10 +321,10 @@ int launch_store(hipStream_t s, int mode, const StoreArgs& a) {
 }
 
 template <int D>
-int launch_store_mt(hipStream_t s, int mt, int mode, const StoreArgs& a) {
-  if (mt == LKV_BF16) return launch_store<D, LKV_BF16>(s, mode, a);
-  if (mt == LKV_F16) return launch_store<D, LKV_F16>(s, mode, a);
-  return launch_store<D, LKV_F32>(s, mode, a);
+int launch_store_mt(hipStream_t s, int mt, int mode, const StoreArgs& a, int64_t max_wgs) {
+  if (mt == LKV_BF16) return launch_store<D, LKV_BF16>(s, mode, a, max_wgs);
+  if (mt == LKV_F16) return launch_store<D, LKV_F16>(s, mode, a, max_wgs);
+  return launch_store<D, LKV_F32>(s, mode, a, max_wgs);
 }
 
 }  // namespace
@@ -382,8 +391,17 @@ extern "C" int lkv_store_blocks(uintptr_t stream, const lkv_kv_source* src, cons
   a.kmax = kmax;
   a.meta_dtype = meta_dtype;
   a.meta_hstride = meta_head_stride;
+  // A host-memory source or destination: a grid that keeps the host budget in flight, one pair
+  // per wave (the kernel strides over the rest).
+  int64_t max_wgs = INT64_MAX;
+  const lkv_kv_source* host_side = (dst && (dst->flags & LKV_SRC_HOST)) ? dst : ((src->flags & LKV_SRC_HOST) ? src : nullptr);
+  if (host_side) {
+    const double budget = host_side == dst ? lkv_host_write_inflight() : lkv_host_read_inflight();
+    max_wgs = (int64_t)(budget / ((double)kWaves * (double)lkv_pair_bytes(host_side, block_size, head_dim)));
+    if (max_wgs < 1) max_wgs = 1;
+  }
   hipStream_t s = (hipStream_t)stream;
-  return head_dim == 128 ? launch_store_mt<128>(s, mt, mode, a) : launch_store_mt<64>(s, mt, mode, a);
+  return head_dim == 128 ? launch_store_mt<128>(s, mt, mode, a, max_wgs) : launch_store_mt<64>(s, mt, mode, a, max_wgs);
 }
 
 extern "C" int lkv_pack_int8(uintptr_t stream, const void* pairs, int dtype, int64_t m, int block_size, int head_dim,
