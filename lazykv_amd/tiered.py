@@ -137,6 +137,46 @@ class TieredLayer:
         self.boundary_d2h_bytes = 0
         return self
 
+    @classmethod
+    def from_store(
+        cls,
+        host: torch.Tensor,
+        n_sealed: int,
+        tail: torch.Tensor,
+        k_blocks: int,
+        block_size: int,
+        capacity_tokens: int,
+        device: torch.device,
+        n_slots: int | None = None,
+        fetch: str = "zerocopy",
+        exact: bool = False,
+        rank_dtype: torch.dtype | None = torch.float32,
+    ) -> TieredLayer:
+        """A layer over a host pool whose first `n_sealed` blocks already hold the sealed KV
+        (lazykv/tiered.py:226-236): a snapshot restore reads them straight into the pool.
+
+        The metadata is rebuilt on the GPU by reading the pool in place (and, for the exact tier,
+        copying it into the HBM store in the same pass); the sink slot is block 0 of the pool and the
+        current slot is `tail` [h, 2, fill, d]. Nothing is written back to the host.
+        """
+        _, h, two, bs, d = host.shape
+        if two != 2 or bs != block_size:
+            raise ValueError(f"host pool {tuple(host.shape)} is not [blocks, h, 2, {block_size}, d]")
+        fill = tail.shape[2]
+        if tuple(tail.shape) != (h, 2, fill, d) or not 0 <= fill <= bs:
+            raise ValueError(f"tail must be [{h}, 2, fill <= {bs}, {d}], got {tuple(tail.shape)}")
+        self = cls.__new__(cls)
+        self._allocate(h, d, n_sealed, k_blocks, bs, capacity_tokens, torch.device(device), host.dtype, host, n_slots, None, fetch, exact, rank_dtype)
+        if n_sealed > 0:
+            src = kernels.pool_source(host)  # read in place over PCIe
+            kernels.store_blocks(src, dst=self._store_src, n_kv=h, head_dim=d, block_size=bs, first_block=0, n_blocks=n_sealed, kmin=self.kmin, kmax=self.kmax)
+            self.pool[0].copy_(host[0])
+        if fill:
+            self.pool[1, :, :, :fill].copy_(tail)
+        self.n_sealed, self.fill, self.length = n_sealed, fill, n_sealed * bs + fill
+        self.boundary_d2h_bytes = 0
+        return self
+
     def _allocate(self, h, d, n_blocks, k_blocks, bs, capacity_tokens, dev, dt, host, n_slots, quant, fetch, exact, rank_dtype, check_budget=True) -> None:  # noqa: ANN001
         if check_budget and n_blocks - 1 <= k_blocks:
             raise ValueError(f"budget of {k_blocks} blocks covers all {n_blocks - 1} candidate blocks; the tier needs selection")
