@@ -135,6 +135,26 @@ int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void*
                       const lkv_kv_source* cur, const lkv_kv_source* rem, void* out, int out_dtype, float* lse,
                       void* ws, size_t ws_bytes);
 
+/* ---- next row: device-side hybrid residency. Replaces rung 6's host-side admit / gather
+ * (lazykv/tiered.py:389-487: the least recently used slots outside the chosen set are the victims,
+ * lazykv/tiered.py:397-418) with device work and no host sync. The reference itself never combined
+ * residency with the zero-copy read. Per KV head, `slots` holds k slots of pairs in HBM; the
+ * tables block_slot[h * block_slot_stride + b] (slot or -1) and slot_block[h * slot_block_stride +
+ * s] (block or -1) say which blocks they hold; the caller allocates them on the device and fills
+ * them with -1 once. Each call first updates the tables for the selection idx: with as many slots
+ * as selected blocks, the slots the selection does not hit are exactly the victims, taken in
+ * ascending slot order by the missed blocks in ascending block order. It then attends as
+ * lkv_sparse_decode does over `host` (mapped host memory, model dtype): a hit is read from its slot
+ * in HBM; a miss is read from `host` and its pair copied into its new slot on the way. The output
+ * and LSE equal lkv_sparse_decode's over `host` bit for bit; only where the bytes come from
+ * differs. desc->k <= 4096, no remainder. */
+size_t lkv_hybrid_decode_workspace_bytes(const lkv_decode_desc* desc);
+int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
+                      const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* idx, int64_t idx_stride,
+                      int32_t* block_slot, int64_t block_slot_stride, int32_t* slot_block, int64_t slot_block_stride,
+                      const lkv_kv_source* sink, const lkv_kv_source* cur, void* out, int out_dtype, float* lse,
+                      void* ws, size_t ws_bytes);
+
 /* ---- a8: exact two-partial merge (lazykv/exact.py:69-85 merge_lse)
  * rows x d outputs (dtype_in) and their LSEs; an empty partial (lse -inf) contributes 0.
  * out/lse may alias out_a/lse_a. */

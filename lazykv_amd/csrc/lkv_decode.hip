@@ -59,7 +59,15 @@ struct DecodeArgs {
   float* lse;
   float* part_ml;  // [n_kv][S][G][2]
   float* part_o;   // [n_kv][S][G][D]
+  // Hybrid residency (optional): loc[h * loc_stride + j] says where selected item j lives -- a slot
+  // of `slots` (a hit), or kLocMiss | slot: read block idx[j] from `sel` (host memory) and copy the
+  // pair into that slot on the way. nullptr: every selected item is read from `sel`.
+  const int32_t* loc;
+  int64_t loc_stride;
+  Src slots;
 };
+
+constexpr int32_t kLocMiss = 0x40000000;
 
 // Raw register image of one chunk (up to 16 tokens) of a pair, exactly as loaded; it is widened
 // to float only when consumed, so a wave can keep two pairs' loads in flight in few registers.
@@ -122,6 +130,38 @@ __device__ __forceinline__ void load_raw(const Src& s, int block, int h, int t0,
     } else {
 #pragma unroll
       for (int w = 0; w < RawModel<D, MT>::W; ++w) raw.k[i][w] = raw.v[i][w] = 0u;
+    }
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void store_words(void* p, const uint32_t (&w)[W]) {
+  if constexpr (W == 1) {
+    *(uint32_t*)p = w[0];
+  } else if constexpr (W == 2) {
+    *(uint2*)p = make_uint2(w[0], w[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) ((uint4*)p)[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  }
+}
+
+// The inverse of load_raw for a model-dtype chunk: the rows this lane loaded, written to `block`
+// of `s` (a slot pool being filled while the pair is attended).
+template <int D, int MT>
+__device__ __forceinline__ void store_raw(const Src& s, int block, int h, int t0, int nit, int r, int c,
+                                          const RawModel<D, MT>& raw) {
+  using T = typename lkv::Elem<MT>::T;
+  constexpr int EPL = D / 16;
+  const int64_t off = (int64_t)block * s.bstride + (int64_t)h * s.hstride + c * EPL;
+  T* kb = (T*)s.k + off;
+  T* vb = (T*)s.v + off;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < nit) {
+      const int row = t0 + r + 4 * i;
+      store_words(kb + (int64_t)row * D, raw.k[i]);
+      store_words(vb + (int64_t)row * D, raw.v[i]);
     }
   }
 }
@@ -320,6 +360,23 @@ __device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, in
   }
 }
 
+// A residency miss: attend `block` of the host source exactly as attend_two does, and copy each
+// chunk it loads into `slot` of the slot pool. Model-dtype sources only (the slots hold the model
+// dtype); the same loads and arithmetic as the zero-copy path, so the result is identical.
+template <int D, int MT, int G>
+__device__ __forceinline__ void attend_fill(const DecodeArgs& a, int block, int slot, int h, const float (&q)[G][D / 16],
+                                            int r, int c, WaveState<D, G>& st) {
+  if (block < 0 || (int64_t)block >= a.sel.nblk || slot < 0 || (int64_t)slot >= a.slots.nblk) return;  // wave-uniform
+#pragma unroll 1
+  for (int t0 = 0; t0 < a.bs; t0 += 16) {
+    const int nit = min(4, (a.bs - t0) >> 2);
+    RawModel<D, MT> raw;
+    load_raw<D, MT>(a.sel, block, h, t0, nit, a.bs, r, c, raw);
+    store_raw<D, MT>(a.slots, slot, h, t0, nit, r, c, raw);
+    consume_chunk<D, G>(q, Widen<D, MT>(raw), raw, t0, nit, a.bs, r, st);
+  }
+}
+
 template <int D, int MT, int G>
 __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
   constexpr int EPL = D / 16;
@@ -362,8 +419,18 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
     const int js = max(first, has_sink) - has_sink;
     const int je = min(last, has_sink + n_sel) - has_sink;
     const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
+    static_assert(kPairs<G> == 1, "the hybrid path below attends one pair per wave per round");
     for (int j = js + wave; j < je; j += kPairs<G> * kWaves) {
       const int b0 = idx_h[j];
+      if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
+        const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
+        if (l >= 0 && (l & kLocMiss)) {
+          attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
+        } else if (l >= 0) {
+          attend_two<D, MT, G>(a, a.slots, l, -1, h, a.bs, q, r, c, st);
+        }
+        continue;
+      }
       const int b1 = (kPairs<G> == 2 && j + kWaves < je) ? idx_h[j + kWaves] : -1;
       attend_two<D, MT, G>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
     }
@@ -596,6 +663,110 @@ int dispatch_g(int g, hipStream_t s, DecodeArgs& a) {
   }
 }
 
+// ---- hybrid residency: which selected blocks are in the HBM slots, and who gets evicted ----------
+// One workgroup per KV head. With as many slots as selected blocks (the reference's default,
+// lazykv/tiered.py:247-250), the victims of a step are exactly the slots its selection does not
+// hit (the least recently used slots outside the chosen set, lazykv/tiered.py:389-418). They are
+// taken in ascending slot order and given to the missed blocks in ascending block order. Tables:
+// block_slot[h][b] = slot or -1, slot_block[h][s] = block or -1. Writes loc[h][j] for the decode:
+// the slot of a hit, kLocMiss | slot for a miss (read from the host, copied into the slot), or -1
+// for an id outside the pool (attended nowhere, like the plain path).
+constexpr int kResThreads = 512;
+constexpr int kMaxSlots = 4096;
+constexpr int kResPer = kMaxSlots / kResThreads;  // items and slots per thread
+
+__device__ __forceinline__ uint32_t res_block_scan(uint32_t v, uint32_t* slots, uint32_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) slots[wave] = x;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kResThreads / 64; ++w) {
+    const uint32_t t = slots[w];
+    if (w < wave) before += t;
+    all += t;
+  }
+  *total = all;
+  return before + x - v;
+}
+
+__global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int k,
+                                                                int32_t* __restrict__ block_slot, int64_t bslot_stride,
+                                                                int64_t n_blocks, int32_t* __restrict__ slot_block,
+                                                                int64_t sblock_stride, int32_t* __restrict__ loc,
+                                                                int64_t loc_stride) {
+  __shared__ uint32_t hit[kMaxSlots / 32];
+  __shared__ int32_t victims[kMaxSlots];
+  __shared__ uint32_t scan_a[kResThreads / 64], scan_b[kResThreads / 64];
+  const int h = blockIdx.x;
+  const int n_slots = k;
+  const int per = (k + kResThreads - 1) / kResThreads;  // <= kResPer
+  const int i0 = threadIdx.x * per;
+  const int32_t* idx_h = idx + (int64_t)h * idx_stride;
+  int32_t* bslot_h = block_slot + (int64_t)h * bslot_stride;
+  int32_t* sblock_h = slot_block + (int64_t)h * sblock_stride;
+  for (int i = threadIdx.x; i < kMaxSlots / 32; i += kResThreads) hit[i] = 0u;
+  // This thread's items [i0, i0 + per): their blocks and current slots.
+  int32_t blk[kResPer], cur[kResPer];
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u) {
+    const int i = i0 + u;
+    blk[u] = (u < per && i < k) ? idx_h[i] : -1;
+    const bool valid = blk[u] >= 0 && (int64_t)blk[u] < n_blocks;
+    cur[u] = valid ? bslot_h[blk[u]] : -2;  // -2: not a block of the pool; -1: not resident
+    if (cur[u] >= n_slots) cur[u] = -1;      // a stale table entry cannot name a slot
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u)
+    if (cur[u] >= 0) atomicOr(&hit[cur[u] >> 5], 1u << (cur[u] & 31));
+  __syncthreads();
+  // Victims: the unhit slots, ascending. Thread t owns slots [t*per, t*per + per).
+  uint32_t free_mask = 0u;
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u) {
+    const int sl = i0 + u;
+    const bool in = u < per && sl < n_slots && !((hit[sl >> 5] >> (sl & 31)) & 1u);
+    free_mask |= (in ? 1u : 0u) << u;
+  }
+  uint32_t n_free;
+  uint32_t vpos = res_block_scan(__popc(free_mask), scan_a, &n_free);
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u) {
+    if ((free_mask >> u) & 1u) victims[vpos++] = i0 + u;
+  }
+  // Misses, ordinal in ascending item (= block) order.
+  uint32_t miss_mask = 0u;
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u) miss_mask |= (cur[u] == -1 ? 1u : 0u) << u;
+  uint32_t n_miss;
+  uint32_t mpos = res_block_scan(__popc(miss_mask), scan_b, &n_miss);  // its barrier also publishes `victims`
+  int32_t* loc_h = loc + (int64_t)h * loc_stride;
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u) {
+    const int i = i0 + u;
+    if (!(u < per && i < k)) continue;
+    if (cur[u] >= 0) {
+      loc_h[i] = cur[u];
+    } else if (cur[u] == -2 || mpos >= n_free) {
+      loc_h[i] = -1;  // outside the pool (or no slot left, which a consistent table rules out)
+    } else {
+      const int v = victims[mpos++];
+      const int32_t old = sblock_h[v];
+      if (old >= 0 && (int64_t)old < n_blocks) bslot_h[old] = -1;  // `old` is unselected: no other item writes it
+      sblock_h[v] = blk[u];
+      bslot_h[blk[u]] = v;
+      loc_h[i] = kLocMiss | v;
+    }
+  }
+}
+
 static Src to_src(const lkv_kv_source* s) {
   Src o{};
   if (s) {
@@ -633,10 +804,19 @@ extern "C" size_t lkv_sparse_decode_workspace_bytes(const lkv_decode_desc* d) {
   return lkv_align_up((size_t)d->n_kv * S * G * 2 * 4, 256) + lkv_align_up((size_t)d->n_kv * S * G * d->head_dim * 4, 256);
 }
 
-extern "C" int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
-                                 const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride,
-                                 const lkv_kv_source* sink, const lkv_kv_source* cur, const lkv_kv_source* rem,
-                                 void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes) {
+// Residency tables of a hybrid call (see residency_kernel).
+struct ResidencyArgs {
+  int32_t* block_slot;
+  int64_t block_slot_stride;
+  int32_t* slot_block;
+  int64_t slot_block_stride;
+};
+
+static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
+                              const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride,
+                              const lkv_kv_source* sink, const lkv_kv_source* cur, const lkv_kv_source* rem,
+                              void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes,
+                              const lkv_kv_source* slots, int32_t* loc, int64_t loc_stride, const ResidencyArgs* res) {
   LKV_CHECK_ARG(desc != nullptr && q != nullptr && out != nullptr && lse != nullptr, "NULL argument");
   const lkv_decode_desc& d = *desc;
   LKV_CHECK_ARG(d.n_kv > 0 && d.n_q > 0 && d.n_q % d.n_kv == 0, "n_q=%d must be a positive multiple of n_kv=%d",
@@ -730,8 +910,17 @@ extern "C" int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, 
   a.part_ml = (float*)w;
   w += lkv_align_up((size_t)d.n_kv * S * G * 2 * 4, 256);
   a.part_o = (float*)w;
+  a.loc = loc;
+  a.loc_stride = loc_stride;
+  if (slots) a.slots = to_src(slots);
 
   hipStream_t s = (hipStream_t)stream;
+  if (res) {  // every argument is checked: update the residency tables, then attend
+    hipLaunchKernelGGL(residency_kernel, dim3(d.n_kv), dim3(kResThreads), 0, s, idx, idx_stride, d.k, res->block_slot,
+                       res->block_slot_stride, sel->n_blocks, res->slot_block, res->slot_block_stride, loc, loc_stride);
+    LKV_CHECK_LAUNCH("residency");
+  }
+
   if (d.head_dim == 128) {
     if (mt == LKV_BF16) return dispatch_g<128, LKV_BF16>(G, s, a);
     if (mt == LKV_F16) return dispatch_g<128, LKV_F16>(G, s, a);
@@ -740,4 +929,43 @@ extern "C" int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, 
   if (mt == LKV_BF16) return dispatch_g<64, LKV_BF16>(G, s, a);
   if (mt == LKV_F16) return dispatch_g<64, LKV_F16>(G, s, a);
   return dispatch_g<64, LKV_F32>(G, s, a);
+}
+
+extern "C" int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
+                                 const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride,
+                                 const lkv_kv_source* sink, const lkv_kv_source* cur, const lkv_kv_source* rem,
+                                 void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes) {
+  return sparse_decode_impl(stream, desc, q, q_dtype, sel, idx, idx_stride, sink, cur, rem, out, out_dtype, lse, ws,
+                            ws_bytes, nullptr, nullptr, 0, nullptr);
+}
+
+extern "C" size_t lkv_hybrid_decode_workspace_bytes(const lkv_decode_desc* d) {
+  const size_t base = lkv_sparse_decode_workspace_bytes(d);
+  if (base == 0) return 0;
+  return base + lkv_align_up((size_t)d->n_kv * (size_t)(d->k > 0 ? d->k : 0) * 4, 256);
+}
+
+extern "C" int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
+                                 const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* idx,
+                                 int64_t idx_stride, int32_t* block_slot, int64_t block_slot_stride, int32_t* slot_block,
+                                 int64_t slot_block_stride, const lkv_kv_source* sink, const lkv_kv_source* cur,
+                                 void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes) {
+  LKV_CHECK_ARG(desc != nullptr && host != nullptr && slots != nullptr && idx != nullptr, "NULL argument");
+  const lkv_decode_desc& d = *desc;
+  LKV_CHECK_ARG(d.attend_selected && d.k > 0, "hybrid decode attends a selection: k > 0 and attend_selected");
+  LKV_CHECK_ARG(d.rem_last == d.rem_first, "hybrid decode has no remainder");
+  LKV_CHECK_ARG(d.k <= kMaxSlots, "k=%d exceeds the hybrid slot limit %d", d.k, kMaxSlots);
+  LKV_CHECK_ARG(d.n_kv > 0 && idx_stride >= d.k, "bad n_kv or idx_stride");
+  LKV_CHECK_ARG(lkv_is_model_dtype(host->dtype) && host->v != nullptr, "the hybrid host pool holds model-dtype pairs");
+  LKV_CHECK_ARG(slots->dtype == host->dtype && slots->k != nullptr && slots->v != nullptr, "slots must match the host pool's dtype");
+  LKV_CHECK_ARG(slots->n_blocks == d.k, "the slot pool holds k=%d slots per head, got %lld", d.k, (long long)slots->n_blocks);
+  LKV_CHECK_ARG(block_slot != nullptr && slot_block != nullptr, "residency tables missing");
+  LKV_CHECK_ARG(block_slot_stride >= host->n_blocks && slot_block_stride >= d.k, "residency table strides too small");
+  const size_t need = lkv_hybrid_decode_workspace_bytes(desc);
+  LKV_CHECK_ARG(ws != nullptr && ws_bytes >= need, "workspace of %zu bytes needed, got %zu", need, ws_bytes);
+  const size_t dec_bytes = lkv_sparse_decode_workspace_bytes(desc);
+  int32_t* loc = (int32_t*)((char*)ws + dec_bytes);  // dec_bytes is a multiple of 256
+  const ResidencyArgs res{block_slot, block_slot_stride, slot_block, slot_block_stride};
+  return sparse_decode_impl(stream, desc, q, q_dtype, host, idx, idx_stride, sink, cur, nullptr, out, out_dtype, lse, ws,
+                            dec_bytes, slots, loc, (int64_t)d.k, &res);
 }

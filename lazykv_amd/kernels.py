@@ -246,6 +246,91 @@ def sparse_decode(
     return out, lse
 
 
+# -- hybrid residency: hits from HBM slots, misses read in place and admitted -------------------------
+
+
+@dataclass
+class Residency:
+    """HBM slots of one layer (`slots` [k, h, 2, bs, d]) and the tables that say what they hold:
+    block_slot [h, cap] (slot or -1), slot_block [h, k] (block or -1), both int32 on the GPU."""
+
+    slots: torch.Tensor
+    block_slot: torch.Tensor
+    slot_block: torch.Tensor
+
+    @classmethod
+    def allocate(cls, k: int, h: int, cap_blocks: int, block_size: int, head_dim: int, dtype: torch.dtype, device: torch.device) -> Residency:
+        return cls(torch.zeros((k, h, 2, block_size, head_dim), dtype=dtype, device=device),
+                   torch.full((h, cap_blocks), -1, dtype=torch.int32, device=device),
+                   torch.full((h, k), -1, dtype=torch.int32, device=device))
+
+
+def hybrid_decode(
+    q: torch.Tensor,
+    *,
+    n_kv: int,
+    block_size: int,
+    scale: float,
+    host: Source,
+    res: Residency,
+    idx: torch.Tensor,
+    sink: Source | None = None,
+    sink_block: int = -1,
+    cur: Source | None = None,
+    cur_block: int = -1,
+    fill: int = 0,
+    out: torch.Tensor | None = None,
+    out_dtype: torch.dtype | None = None,
+    lse: torch.Tensor | None = None,
+    ws: Workspace | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """lkv_hybrid_decode: `sparse_decode` over `host` with the selected pairs in `res`'s slots read
+    from HBM, the others read in place and admitted. Updates `res`'s tables."""
+    p = PreparedHybridDecode(q, n_kv=n_kv, block_size=block_size, scale=scale, host=host, res=res, idx=idx, sink=sink, sink_block=sink_block,
+                             cur=cur, cur_block=cur_block, fill=fill, out=out, out_dtype=out_dtype, lse=lse, ws=ws)
+    p()
+    return p.out, p.lse
+
+
+class PreparedHybridDecode:
+    """`hybrid_decode` with its arguments converted once; `desc.fill` / `desc.cur_block` may change between calls."""
+
+    def __init__(self, q: torch.Tensor, *, n_kv: int, block_size: int, scale: float, host: Source, res: Residency, idx: torch.Tensor, sink: Source | None,
+                 sink_block: int, cur: Source | None, cur_block: int, fill: int, out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                 lse: torch.Tensor | None = None, ws: Workspace | None = None) -> None:
+        _lib.require_cuda(q, idx, res.slots, res.block_slot, res.slot_block)
+        qq = q.reshape(-1, q.shape[-1]).contiguous()
+        n_q, d = qq.shape
+        if idx.dtype != torch.int32 or idx.ndim != 2 or idx.shape[0] != n_kv or not idx.is_contiguous():
+            raise ValueError(f"idx must be contiguous int32 [{n_kv}, k], got {tuple(idx.shape)} {idx.dtype}")
+        k = idx.shape[1]
+        for t, shape in ((res.block_slot, (n_kv, host.n_blocks)), (res.slot_block, (n_kv, k))):
+            if t.dtype != torch.int32 or t.ndim != 2 or tuple(t.shape[:1]) != shape[:1] or t.shape[1] < shape[1] or t.stride(1) != 1:
+                raise ValueError(f"residency table must be int32 [{shape[0]}, >= {shape[1]}] with contiguous rows, got {tuple(t.shape)} {t.dtype}")
+        if res.slots.shape[0] != k:
+            raise ValueError(f"the slot pool must hold k={k} slots, got {res.slots.shape[0]}")
+        out_dtype = out_dtype or (out.dtype if out is not None else qq.dtype)
+        self.out = out if out is not None else torch.empty((n_q, d), dtype=out_dtype, device=q.device)
+        self.lse = lse if lse is not None else torch.empty((n_q,), dtype=torch.float32, device=q.device)
+        self.desc = _lib.DecodeDesc(n_q, n_kv, d, block_size, float(scale), k, 1, sink_block, cur_block, fill, 0, 0)
+        ws = ws or default_workspace(q.device)
+        ws_ptr, ws_n = ws.get(_lib.lib().lkv_hybrid_decode_workspace_bytes(ctypes.byref(self.desc)))
+        slot_src = pool_source(res.slots)
+        self._c = [s.c() if s is not None else None for s in (host, slot_src, sink, cur)]
+        refs = [ctypes.byref(c) if c is not None else None for c in self._c]
+        self._keep = (qq, idx, self.out, self.lse, ws.buf, host, res, sink, cur)
+        self._fn = _lib.lib().lkv_hybrid_decode
+        self._args = (ctypes.byref(self.desc), qq.data_ptr(), _lib.dtype_code(qq.dtype), refs[0], refs[1], idx.data_ptr(), idx.stride(0),
+                      res.block_slot.data_ptr(), res.block_slot.stride(0), res.slot_block.data_ptr(), res.slot_block.stride(0), refs[2], refs[3],
+                      self.out.data_ptr(), _lib.dtype_code(self.out.dtype), self.lse.data_ptr(), ws_ptr, ws_n)
+        self.device = q.device
+
+    def __call__(self) -> None:
+        rc = self._fn(torch.cuda.current_stream(self.device).cuda_stream, *self._args)
+        if rc:
+            _lib.check(rc, "hybrid_decode")
+
+
 # -- a8: merge --------------------------------------------------------------------------------------
 
 

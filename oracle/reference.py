@@ -20,6 +20,9 @@ How each function is pinned (each check lives in `tests/test_oracle.py`):
 * `top_blocks`: brute-force sort; tie order (lower block id first) is this build's rule.
 * `block_minmax`, `current_block_mask`, `blocks_for_budget`: closed forms and the reference's
   own known answers (`tests/test_selection.py:38-44,98`).
+* `residency_step`: invariants that fix it (after a step the resident set is exactly the chosen
+  set, hits keep their slots, victims are exactly the unhit slots) and a least-recently-used
+  simulation in the reference's own terms (lazykv/tiered.py:389-418), on random step sequences.
 * `attend` / `partial_attention` / `merge_lse`: float64 brute force over explicit token lists,
   the reference's merge known answer (`tests/test_exact.py:72-84`), the empty-partial rule
   (`tests/test_exact.py:52-69`) and the two-halves reconstruction (`tests/test_exact.py:32-49`).
@@ -324,3 +327,43 @@ def partial_attention(keys: np.ndarray, values: np.ndarray, query: np.ndarray, s
     with np.errstate(divide="ignore"):
         lse = np.where(empty, -np.inf, m + np.log(norm)).squeeze(-1)
     return out, lse
+
+
+# -- hybrid residency (device-side rung 6): which selected blocks sit in the HBM slots ------------
+
+LOC_MISS = 0x40000000
+
+
+def residency_step(block_slot: np.ndarray, slot_block: np.ndarray, chosen: np.ndarray) -> np.ndarray:
+    """One step of the hybrid tier's residency, per KV head, with as many slots as chosen blocks.
+
+    Follows lazykv/tiered.py:389-418 (admit): hits keep their slots and the victims are the least
+    recently used slots outside the chosen set, which with k slots and k chosen blocks is exactly the
+    set of slots the choice does not hit. Victims are taken in ascending slot order by the missed
+    blocks in ascending block order (the reference hands them out in rank order; the order only
+    moves a block between slots, never changes what is attended). Updates block_slot [h, cap] and
+    slot_block [h, k] in place (-1 = empty) and returns loc [h, k]: the slot of a hit, or
+    LOC_MISS | slot for a miss read from the host and copied into that slot.
+    """
+    h, k = chosen.shape
+    loc = np.empty((h, k), dtype=np.int64)
+    for j in range(h):
+        cur = block_slot[j, chosen[j]]
+        hit_slots = set(int(s) for s in cur if s >= 0)
+        victims = [s for s in range(slot_block.shape[1]) if s not in hit_slots]
+        order = np.argsort(chosen[j], kind="stable")
+        m = 0
+        for i in order:
+            b = int(chosen[j, i])
+            if cur[i] >= 0:
+                loc[j, i] = cur[i]
+                continue
+            v = victims[m]
+            m += 1
+            old = slot_block[j, v]
+            if old >= 0:
+                block_slot[j, old] = -1
+            slot_block[j, v] = b
+            block_slot[j, b] = v
+            loc[j, i] = LOC_MISS | v
+    return loc

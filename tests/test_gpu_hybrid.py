@@ -1,0 +1,73 @@
+"""Device-side hybrid residency on the GPU: over a drifting sequence of decode steps, the hybrid
+decode's output and LSE equal the zero-copy decode's bit for bit, its residency tables equal the
+oracle's (oracle.reference.residency_step), and every slot holds an exact copy of its block."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(seed: int, h: int, g: int, n: int, bs: int, d: int, dt: torch.dtype):  # noqa: ANN202
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+    from lazykv_amd.workload import draw_layer, to_pool
+
+    w = draw_layer(seed, h * g, h, d, n * bs, bs, dt)
+    pool = to_pool(w.keys, w.values, bs).cuda()
+    kmin = torch.zeros((1, h, n, d), dtype=dt, device="cuda")
+    kmax = torch.zeros_like(kmin)
+    kernels.store_blocks(kernels.dense_source(w.keys.cuda(), w.values.cuda(), bs), n_kv=h, head_dim=d, block_size=bs, first_block=0, n_blocks=n - 1, kmin=kmin, kmax=kmax)
+    host = pinned_empty(tuple(pool.shape), dt)
+    host.copy_(pool)
+    return w, pool, host, kmin, kmax
+
+
+@pytest.mark.parametrize(("h", "g", "n", "bs", "d", "k", "dt", "fill"), [(8, 4, 300, 16, 128, 32, torch.bfloat16, 16), (4, 4, 200, 16, 64, 24, torch.float16, 5), (2, 8, 150, 32, 128, 40, torch.bfloat16, 19)])
+def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, fill: int) -> None:
+    from lazykv_amd import kernels
+
+    w, pool, host, kmin, kmax = _layer(n + k, h, g, n, bs, d, dt)
+    res = kernels.Residency.allocate(k, h, n, bs, d, dt, torch.device("cuda"))
+    bs_ref = np.full((h, n), -1, dtype=np.int64)
+    sb_ref = np.full((h, k), -1, dtype=np.int64)
+    slots_src = pool[[0, n - 1]].contiguous()
+    ss = kernels.pool_source(slots_src)
+    hsrc = kernels.pool_source(host)
+    gen = torch.Generator().manual_seed(5)
+    q0 = w.query.float()
+    hits = 0
+    for step in range(12):
+        q = (q0 + 0.35 * torch.randn(q0.shape, generator=gen)).to(dt).cuda()
+        idx = kernels.bound_topk(q, kmin, kmax, k, cand_offset=1, n_cand=n - 2)
+        common = dict(n_kv=h, block_size=bs, scale=d**-0.5, idx=idx, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=fill, out_dtype=torch.float32)
+        out_z, lse_z = kernels.sparse_decode(q, sel=hsrc, **common)
+        out_h, lse_h = kernels.hybrid_decode(q, host=hsrc, res=res, **common)
+        torch.cuda.synchronize()
+        assert torch.equal(out_h, out_z) and torch.equal(lse_h, lse_z), step
+        chosen = idx.cpu().numpy().astype(np.int64)
+        prev = bs_ref.copy()
+        R.residency_step(bs_ref, sb_ref, chosen)
+        assert np.array_equal(res.block_slot.cpu().numpy(), bs_ref), step
+        assert np.array_equal(res.slot_block.cpu().numpy(), sb_ref), step
+        hits += int((np.take_along_axis(prev, chosen, axis=1) >= 0).sum())
+        # every slot holds an exact copy of the block the table names
+        for j in range(h):
+            assert torch.equal(res.slots[:, j], pool[torch.from_numpy(sb_ref[j]).cuda(), j])
+    assert hits > 0  # the drift keeps part of each selection resident
+
+
+def test_hybrid_decode_refuses_what_it_cannot_hold() -> None:
+    from lazykv_amd import kernels
+
+    h, g, n, bs, d, k = 2, 4, 60, 16, 64, 8
+    w, pool, host, kmin, kmax = _layer(1, h, g, n, bs, d, torch.float16)
+    idx = kernels.bound_topk(w.query.cuda(), kmin, kmax, k, cand_offset=1, n_cand=n - 2)
+    wrong = kernels.Residency.allocate(k + 1, h, n, bs, d, torch.float16, torch.device("cuda"))
+    with pytest.raises(ValueError, match="slots"):
+        kernels.hybrid_decode(w.query.cuda(), n_kv=h, block_size=bs, scale=d**-0.5, host=kernels.pool_source(host), res=wrong, idx=idx)

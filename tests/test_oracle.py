@@ -294,3 +294,62 @@ def test_excluding_a_block_removes_exactly_that_block() -> None:
         keep = [t for t in range(n_blocks * bs) if not (drop * bs <= t < (drop + 1) * bs)]
         o, _ = _brute_softmax(query[j, 0], keys[j, keep], values[j, keep], d**-0.5)
         assert np.allclose(out[j, 0], o, atol=1e-10)
+
+
+# -- hybrid residency ---------------------------------------------------------------------------------
+
+
+def _lru_reference(steps: list[np.ndarray], n_blocks: int, k: int) -> list[set[int]]:
+    """The reference's admit (lazykv/tiered.py:389-418) for one head: victims are the least recently
+    used slots outside the chosen set (empty slots first, ties to the lower slot); returns the
+    resident block set after each step."""
+    slot_block = [-1] * k
+    last_used = [-2] * k
+    out = []
+    for step, chosen in enumerate(steps):
+        where = {b: s for s, b in enumerate(slot_block) if b >= 0}
+        keep = {where[b] for b in chosen.tolist() if b in where}
+        misses = [b for b in chosen.tolist() if b not in where]
+        free = sorted((s for s in range(k) if s not in keep), key=lambda s: (last_used[s], s))
+        for b, s in zip(misses, free):
+            slot_block[s] = b
+        for b in chosen.tolist():
+            last_used[slot_block.index(b)] = step
+        out.append({b for b in slot_block if b >= 0})
+    return out
+
+
+def test_residency_step_keeps_hits_and_evicts_exactly_the_unhit_slots() -> None:
+    rng = np.random.default_rng(3)
+    h, n, k = 3, 60, 8
+    block_slot = np.full((h, n), -1, dtype=np.int64)
+    slot_block = np.full((h, k), -1, dtype=np.int64)
+    seqs = [[] for _ in range(h)]
+    chosen = np.stack([np.sort(rng.choice(n, k, replace=False)) for _ in range(h)])
+    for _ in range(40):
+        # drift: each step keeps most of the previous choice
+        nxt = []
+        for j in range(h):
+            keep = rng.choice(chosen[j], k - 3, replace=False)
+            pool = np.setdiff1d(np.arange(n), keep)
+            nxt.append(np.sort(np.concatenate([keep, rng.choice(pool, 3, replace=False)])))
+        prev_bs, prev_sb = block_slot.copy(), slot_block.copy()
+        chosen = np.stack(nxt)
+        loc = R.residency_step(block_slot, slot_block, chosen)
+        for j in range(h):
+            seqs[j].append(chosen[j])
+            assert set(slot_block[j].tolist()) == set(chosen[j].tolist())  # resident set == chosen set
+            for s in range(k):
+                assert block_slot[j, slot_block[j, s]] == s
+            assert (block_slot[j] >= 0).sum() == k
+            hits = [i for i in range(k) if prev_bs[j, chosen[j, i]] >= 0]
+            for i in hits:  # a hit keeps its slot and is read from it
+                assert loc[j, i] == prev_bs[j, chosen[j, i]] and not loc[j, i] & R.LOC_MISS
+            misses = [i for i in range(k) if i not in hits]
+            victims = sorted(int(loc[j, i]) & ~R.LOC_MISS for i in misses)
+            assert victims == sorted(set(range(k)) - {int(prev_bs[j, chosen[j, i]]) for i in hits})
+            # victims go to the misses in ascending block order, in ascending slot order
+            assert [int(loc[j, i]) & ~R.LOC_MISS for i in sorted(misses, key=lambda i: chosen[j, i])] == victims
+            assert all(prev_sb[j, v] not in chosen[j] for v in victims)
+    for j in range(h):
+        assert _lru_reference(seqs[j], n, k)[-1] == set(slot_block[j].tolist())
