@@ -9,16 +9,19 @@ What a selecting layer does per decode step, with no host synchronisation anywhe
    K per KV head on the device (lazykv/tiered.py:383-387, without the `.cpu()`).
 3. `decode` attends sink + selected + current[:fill] in one block-sparse kernel that reads each
    selected pair where it lives: in place from the mapped host pool over PCIe (`fetch="zerocopy"`,
-   lazykv/tiered.py:489-511) or from an HBM store (`fetch="resident"`, all blocks on the GPU as
-   in rung 5, lazykv/selection.py:147-183). With `exact=True` the same kernel also attends every
+   lazykv/tiered.py:489-511), from an HBM store (`fetch="resident"`, all blocks on the GPU as
+   in rung 5, lazykv/selection.py:147-183), or from HBM slots holding the k most recently selected
+   blocks per head, the misses read in place and admitted as they are attended (`fetch="hybrid"`,
+   the device-side form of rung 6's admit/gather, lazykv/tiered.py:389-487; bit-identical to the
+   zero-copy result). With `exact=True` the same kernel also attends every
    other sealed block from the host tier and merges the two partials by log-sum-exp
    (lazykv/exact.py:225-264), so the result is full attention.
 
 Layouts follow the reference: GPU slot pool [2, h, 2, bs, d] holding the sink (slot 0) and the
 current block (slot 1) (`n_slots=0`, lazykv/tiered.py:250,261); host pool [cap, h, 2, bs, d] in
 the model dtype or [cap, h, P] int8 records (:265); metadata [1, h, cap, d] in the model dtype
-(:262), taken over the dequantised keys for an int8 tier (:182-194). The residency machinery of
-rungs 6-7 (slots, admit, prefetch) is not part of this path.
+(:262), taken over the dequantised keys for an int8 tier (:182-194). Rung 7's speculative
+prefetch and the host-side residency tables of rung 6 are not part of this path.
 """
 
 from __future__ import annotations
@@ -37,7 +40,7 @@ from lazykv_amd.pinned import pinned_empty
 from lazykv_amd.quant import packed_pair_bytes
 from lazykv_amd.selection import QUEST_DENSE_LAYERS
 
-FETCH_MODES = ("zerocopy", "resident")
+FETCH_MODES = ("zerocopy", "resident", "hybrid")
 
 
 @dataclass
@@ -132,7 +135,7 @@ class TieredLayer:
     ) -> TieredLayer:
         """An empty layer whose pools the caller fills (`load_blocks`, `set_current`), e.g. a restore."""
         self = cls.__new__(cls)
-        self._allocate(h, d, capacity_tokens // block_size, k_blocks, block_size, capacity_tokens, device, dtype, host, 0, quant, fetch, exact, rank_dtype, check_budget=False)
+        self._allocate(h, d, capacity_tokens // block_size, k_blocks, block_size, capacity_tokens, device, dtype, host, None, quant, fetch, exact, rank_dtype, check_budget=False)
         self.n_sealed, self.fill, self.length = 0, 0, 0
         self.boundary_d2h_bytes = 0
         return self
@@ -180,7 +183,12 @@ class TieredLayer:
     def _allocate(self, h, d, n_blocks, k_blocks, bs, capacity_tokens, dev, dt, host, n_slots, quant, fetch, exact, rank_dtype, check_budget=True) -> None:  # noqa: ANN001
         if check_budget and n_blocks - 1 <= k_blocks:
             raise ValueError(f"budget of {k_blocks} blocks covers all {n_blocks - 1} candidate blocks; the tier needs selection")
-        if n_slots not in (None, 0):
+        if fetch == "hybrid":
+            if n_slots not in (None, k_blocks):
+                raise ValueError(f"the hybrid tier keeps one HBM slot per selected block: n_slots must be k_blocks={k_blocks}")
+            if quant is not None:
+                raise ValueError("the hybrid tier's slots hold the model dtype: an int8 host tier needs fetch='zerocopy'")
+        elif n_slots not in (None, 0):
             raise ValueError("the GPU tier holds only the sink and the current block in slots (n_slots=0)")
         if quant not in (None, "int8"):
             raise ValueError(f"unknown tier precision {quant!r}")
@@ -201,7 +209,7 @@ class TieredLayer:
         self.kmin = torch.zeros((1, h, self.cap_blocks, d), dtype=dt, device=dev)
         self.kmax = torch.zeros_like(self.kmin)
         self.logical_pair_bytes = 2 * bs * d * self.pool.element_size()
-        need_host = fetch == "zerocopy" or exact
+        need_host = fetch in ("zerocopy", "hybrid") or exact
         shape = (self.cap_blocks, h, 2, bs, d) if quant is None else (self.cap_blocks, h, packed_pair_bytes(bs, d))
         want = dt if quant is None else torch.uint8
         if host is None and need_host:
@@ -215,6 +223,8 @@ class TieredLayer:
         if host is not None:
             self._host_src = kernels.pool_source(host) if quant is None else kernels.record_source(host, dt)
         self._store_src = kernels.pool_source(self.store) if self.store is not None else None
+        # Hybrid: the k most recently selected blocks per head, in HBM slots (empty at first).
+        self.res = kernels.Residency.allocate(k_blocks, h, self.cap_blocks, bs, d, dt, dev) if fetch == "hybrid" else None
         self._pool_src = kernels.pool_source(self.pool)
 
     # -- writes ---------------------------------------------------------------------------------
@@ -306,6 +316,11 @@ class TieredLayer:
         if self.exact:
             rem, rem_range = self._host_src, (1, n_full)
         scale = scaling if scaling is not None else self.d**-0.5
+        if self.res is not None:
+            return kernels.hybrid_decode(
+                query.reshape(-1, self.d), n_kv=self.h, block_size=self.bs, scale=scale, host=self._host_src, res=self.res, idx=idx,
+                sink=self._pool_src, sink_block=0, cur=self._pool_src, cur_block=1 if fill > 0 else -1, fill=fill, out=out, lse=lse, ws=ws,
+            )
         return kernels.sparse_decode(
             query.reshape(-1, self.d), n_kv=self.h, block_size=self.bs, scale=scale, sel=sel, idx=idx,
             sink=self._pool_src, sink_block=0, cur=self._pool_src, cur_block=1 if fill > 0 else -1, fill=fill,
@@ -314,7 +329,8 @@ class TieredLayer:
 
     def gpu_bytes(self) -> int:
         store = self.store.numel() * self.store.element_size() if self.store is not None else 0
-        return self.pool.numel() * self.pool.element_size() + store
+        slots = self.res.slots.numel() * self.res.slots.element_size() if self.res is not None else 0
+        return self.pool.numel() * self.pool.element_size() + store + slots
 
     def metadata_bytes(self) -> int:
         return 2 * self.kmin.numel() * self.kmin.element_size()

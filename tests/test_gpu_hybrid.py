@@ -71,3 +71,36 @@ def test_hybrid_decode_refuses_what_it_cannot_hold() -> None:
     wrong = kernels.Residency.allocate(k + 1, h, n, bs, d, torch.float16, torch.device("cuda"))
     with pytest.raises(ValueError, match="slots"):
         kernels.hybrid_decode(w.query.cuda(), n_kv=h, block_size=bs, scale=d**-0.5, host=kernels.pool_source(host), res=wrong, idx=idx)
+
+
+def test_hybrid_cache_decodes_like_the_zero_copy_cache() -> None:
+    """A transformers Llama stack decoding 40 tokens through seals: the hybrid tier's
+    log-probabilities equal the zero-copy tier's bit for bit."""
+    import copy
+
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from lazykv_amd.attention import IMPLEMENTATION_NAME, install
+    from lazykv_amd.tiered_prefill import tiered_prefill
+
+    install()
+    torch.manual_seed(0)
+    cfg = LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=4, num_attention_heads=4, num_key_value_heads=2, head_dim=64, vocab_size=512, max_position_embeddings=4096)
+    with torch.device("cuda"):
+        model = LlamaForCausalLM(copy.deepcopy(cfg))
+    model.set_attn_implementation(IMPLEMENTATION_NAME)
+    model = model.to(dtype=torch.float16).eval()
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    ids = torch.randint(0, cfg.vocab_size, (1, 140), device="cuda", generator=gen)
+    caches = {}
+    for fetch in ("zerocopy", "hybrid"):
+        got = tiered_prefill(model, ids[:, :100], 32, 3, 16, 512, dense_layers=1, fetch=fetch)
+        rows = [torch.log_softmax(got.last_logits, -1)]
+        with torch.inference_mode():
+            for t in range(100, 140):
+                out = model(input_ids=ids[:, t : t + 1], past_key_values=got.cache, use_cache=True, **got.cache.model_kwargs())
+                rows.append(torch.log_softmax(out.logits[0, -1].float(), -1))
+        caches[fetch] = (torch.stack(rows), got.cache)
+    assert torch.equal(caches["zerocopy"][0], caches["hybrid"][0])
+    tier = caches["hybrid"][1].tiers[1]
+    assert tier.res is not None and (tier.res.block_slot >= 0).any()
