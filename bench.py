@@ -665,7 +665,8 @@ def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
                                f"float16 weights ~N(0,0.02), chunks of {chunk}, every layer's KV into the int8 host tier (dense_layers 0)",
                    "layers": L, "tokens": n, "q_heads": N_Q, "kv_heads": H, "head_dim": d, "block_size": BS, "k": k, "chunk": chunk, "dense_layers": 0},
         "roofline": {"bound": "pcie", "kernel": "store_blocks_kernel (int8 records to host + metadata of the dequantised keys)", "achieved": round(pcie, 2),
-                     "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(pcie / PCIE_PEAK_GBPS, 4), "traffic": None,
+                     "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(pcie / PCIE_PEAK_GBPS, 4), "traffic": pmc_traffic().get("prefill/store_blocks_kernel"),
+                     "traffic_note": f"calibrated FETCH_SIZE + WRITE_SIZE bytes per launch (K/V read + records and metadata written), algorithmic {b_read + b_rec + b_meta}; source {TRAFFIC_FILE.relative_to(ROOT)}",
                      "algorithmic_bytes": b_rec, "kernel_us": round(boundary_us, 2),
                      "hbm_read_bytes": b_read, "hbm_read_gbps": round(b_read / (boundary_us * 1e-6) / 1e9, 1), "metadata_bytes": b_meta},
         "byte_roofline": {"hbm_bytes_per_layer": b_read + b_meta, "pcie_bytes_per_layer": b_rec, "t_roof_us_at_64gbps": round(t_roof, 2),
