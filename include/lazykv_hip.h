@@ -104,7 +104,8 @@ int lkv_host_free(void* host_ptr);
 int lkv_host_device_pointer(const void* host_ptr, void** dev_ptr);
 
 /* ---- a1 + a2: Quest bound and on-device top-K (lazykv/selection.py:38-62; call sites
- * lazykv/tiered.py:383-387 rank and :500 gather_zerocopy)
+ * lazykv/tiered.py:383-387 rank and :500 gather_zerocopy). Up to 262,144 candidates per KV head
+ * (4M tokens at 16-token blocks); past 12,288 the selection re-reads the bounds on each pass.
  * q [n_q, d] (q_dtype); kmin/kmax: block metadata of KV head h, block b at
  * meta + h*meta_head_stride + b*d (meta_dtype elements). Candidates are blocks
  * cand_offset .. cand_offset+n_cand-1. Writes, per KV head, the ids (cand_offset included, the

@@ -394,6 +394,207 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
   }
 }
 
+// ---- select for long contexts: keys streamed from memory on every pass --------------------------
+// The same selection as select_kernel -- range-adaptive radix select of the K-th largest key, direct
+// ranking of the boundary bin, ties to the lower id, ascending or sorted output -- for heads with
+// more candidates than the registers hold (kMaxCand). Thread t owns the contiguous run
+// [t * npt, (t + 1) * npt) and re-reads its bounds (L2-resident after the first pass) on each pass.
+constexpr int kMaxStreamCand = 1 << 18;  // 262,144 candidates per head: 4M tokens at 16-token blocks
+
+__global__ __launch_bounds__(kSelThreads) void select_stream_kernel(const float* __restrict__ bounds, int64_t bstride,
+                                                                    int n_cand, int k, int cand_offset, int sorted,
+                                                                    int32_t* __restrict__ out_idx, int64_t idx_stride) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t list[2 * kSelThreads];
+  __shared__ uint32_t taken[kMaxStreamCand / 32];
+  __shared__ __align__(16) uint32_t stage[kStage];
+  __shared__ uint32_t mm[2 * kSelWaves];
+  __shared__ uint32_t scan_pass[kSelWaves], scan_out[kSelWaves];
+  __shared__ uint32_t info[4];
+  const int h = blockIdx.x;
+  const int n = n_cand;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int npt = (n + kSelThreads - 1) / kSelThreads;
+  const int i0 = threadIdx.x * npt;
+  const int i1 = min(n, i0 + npt);
+  const float* bound_h = bounds + (int64_t)h * bstride;
+  for (int i = threadIdx.x; i < (n + 31) / 32; i += kSelThreads) taken[i] = 0u;
+  uint32_t lmin = 0xffffffffu, lmax = 0u;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t key = orderable(bound_h[i]);
+    lmin = min(lmin, key);
+    lmax = max(lmax, key);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lmin = min(lmin, (uint32_t)__shfl_xor(lmin, o, 64));
+    lmax = max(lmax, (uint32_t)__shfl_xor(lmax, o, 64));
+  }
+  if (lane == 0) {
+    mm[2 * wave] = lmin;
+    mm[2 * wave + 1] = lmax;
+  }
+  __syncthreads();
+  uint32_t lo = mm[0], hi = mm[1];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    lo = min(lo, mm[2 * w]);
+    hi = max(hi, mm[2 * w + 1]);
+  }
+  int need = k;
+  uint32_t T;
+  bool ranked = false;  // the boundary bin was ranked directly: its best keys are marked in `taken`
+#pragma unroll 1
+  while (true) {
+    if (lo >= hi) {
+      T = lo;
+      break;
+    }
+    const uint32_t width = hi - lo;
+    const int bits = 32 - __clz(width);
+    const int shift = bits > 11 ? bits - 11 : 0;
+    const int nb = (int)(width >> shift) + 1;
+    for (int i = threadIdx.x; i < nb; i += kSelThreads) hist[i] = 0;
+    __syncthreads();
+    for (int i = i0; i < i1; ++i) {
+      const uint32_t key = orderable(bound_h[i]);
+      if (key >= lo && key <= hi) atomicAdd(&hist[(key - lo) >> shift], 1u);
+    }
+    __syncthreads();
+    const int per = (nb + kSelThreads - 1) / kSelThreads;
+    uint32_t local = 0;
+    for (int j = 0; j < per; ++j) {
+      const int bin = threadIdx.x * per + j;
+      if (bin < nb) local += hist[bin];
+    }
+    uint32_t total;
+    const uint32_t below = block_exclusive_scan(local, scan_pass, &total);
+    const uint32_t above = total - below - local;
+    if (above < (uint32_t)need && (uint32_t)need <= above + local) {
+      uint32_t acc = above;
+      for (int j = per - 1; j >= 0; --j) {
+        const int bin = threadIdx.x * per + j;
+        const uint32_t cnt = bin < nb ? hist[bin] : 0u;
+        if ((uint32_t)need <= acc + cnt) {
+          info[0] = (uint32_t)bin;
+          info[1] = acc;
+          info[2] = cnt;
+          info[3] = 0u;
+          break;
+        }
+        acc += cnt;
+      }
+    }
+    __syncthreads();
+    const uint32_t bin = info[0];
+    need -= (int)info[1];
+    const uint32_t in_bin = info[2];
+    const uint32_t new_lo = lo + (bin << shift);
+    const uint32_t span = shift ? ((1u << shift) - 1u) : 0u;
+    hi = min(hi, new_lo + span);
+    lo = new_lo;
+    if (lo < hi && in_bin <= (uint32_t)kSelThreads) {
+      uint32_t* list_key = list;
+      uint32_t* list_id = list + kSelThreads;
+      for (int i = i0; i < i1; ++i) {
+        const uint32_t key = orderable(bound_h[i]);
+        if (key >= lo && key <= hi) {
+          const uint32_t slot = atomicAdd(&info[3], 1u);
+          list_key[slot] = key;
+          list_id[slot] = (uint32_t)i;
+        }
+      }
+      __syncthreads();
+      const int m = (int)info[3];
+      if ((int)threadIdx.x < m) {
+        const uint32_t mk = list_key[threadIdx.x], mi = list_id[threadIdx.x];
+        int rank = 0;
+        for (int e = 0; e < m; ++e) {
+          const uint32_t ek = list_key[e], ei = list_id[e];
+          rank += (ek > mk) | ((ek == mk) & (ei < mi));
+        }
+        if (rank < need) atomicOr(&taken[mi >> 5], 1u << (mi & 31));
+      }
+      __syncthreads();
+      T = hi;
+      need = 0;
+      ranked = true;
+      break;
+    }
+    __syncthreads();
+  }
+
+  // ---- compaction: ascending id, ties (== T, unmarked) taken in index order ---------------------
+  uint32_t gt = 0, eq = 0;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t key = orderable(bound_h[i]);
+    const bool mk = ranked && ((taken[i >> 5] >> (i & 31)) & 1u);
+    gt += (key > T) | mk;
+    eq += (key == T) & !mk;
+  }
+  uint32_t tot;
+  const uint32_t before_gt = block_exclusive_scan(gt, scan_out, &tot);
+  __syncthreads();  // scan_out is reused just below
+  const uint32_t before_eq = block_exclusive_scan(eq, scan_out, &tot);
+  int take_eq = need - (int)before_eq;
+  take_eq = take_eq < 0 ? 0 : (take_eq > (int)eq ? (int)eq : take_eq);
+  const uint32_t pos0 = before_gt + (uint32_t)min((int)before_eq, need);
+  int32_t* out_h = out_idx + (int64_t)h * idx_stride;
+  uint64_t* sortbuf = reinterpret_cast<uint64_t*>(stage);
+  for (int base = 0; base < (sorted ? 1 : k); base += kStage) {
+    const uint32_t lim = sorted ? (uint32_t)k : (uint32_t)min(base + kStage, k);
+    uint32_t pos = pos0;
+    int taken_eq = 0;
+    for (int i = i0; i < i1; ++i) {
+      const uint32_t key = orderable(bound_h[i]);
+      const bool mk = ranked && ((taken[i >> 5] >> (i & 31)) & 1u);
+      bool take = (key > T) || mk;
+      if (!take && key == T && taken_eq < take_eq) {
+        take = true;
+        ++taken_eq;
+      }
+      if (take) {
+        if (pos >= (uint32_t)base && pos < lim) {
+          if (sorted) {
+            sortbuf[pos] = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+          } else {
+            stage[pos - base] = (uint32_t)i;
+          }
+        }
+        ++pos;
+      }
+    }
+    __syncthreads();
+    if (sorted) break;
+    for (int i = threadIdx.x; i < kStage && base + i < k; i += kSelThreads) out_h[base + i] = (int32_t)stage[i] + cand_offset;
+    __syncthreads();
+  }
+  if (!sorted) return;
+  int kp2 = 1;
+  while (kp2 < k) kp2 <<= 1;
+  for (int i = k + threadIdx.x; i < kp2; i += kSelThreads) sortbuf[i] = 0;
+  __syncthreads();
+  for (int size = 2; size <= kp2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < kp2 / 2; t += kSelThreads) {
+        const int a = 2 * t - (t & (stride - 1));
+        const int b = a + stride;
+        const bool desc = (a & size) == 0;
+        const uint64_t x = sortbuf[a], y = sortbuf[b];
+        if ((x < y) == desc) {
+          sortbuf[a] = y;
+          sortbuf[b] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = threadIdx.x; i < k; i += kSelThreads) {
+    const uint32_t id = 0xffffffffu - (uint32_t)(sortbuf[i] & 0xffffffffu);
+    out_h[i] = (int32_t)id + cand_offset;
+  }
+}
+
 template <int D, int MT, int G>
 int launch_bound(hipStream_t stream, const void* q, int q_dtype, const void* kmin, const void* kmax, int64_t mhs, int n_kv,
                  int cand_offset, int n_cand, int rank_mode, float* bounds, int64_t bstride) {
@@ -441,8 +642,8 @@ extern "C" int lkv_bound_topk(uintptr_t stream, const void* q, int q_dtype, cons
   LKV_CHECK_ARG(meta_head_stride >= (int64_t)(cand_offset + n_cand) * head_dim, "metadata head stride too small");
   LKV_CHECK_ARG(k == 0 || (out_idx != nullptr && idx_stride >= k), "out_idx missing or idx_stride < k");
   const int sorted = (flags & LKV_SORTED) ? 1 : 0;
-  if (k > 0 && n_cand > kMaxCand) {
-    lkv_set_error("%d candidate blocks exceed the per-head select limit %d", n_cand, kMaxCand);
+  if (k > 0 && n_cand > kMaxStreamCand) {
+    lkv_set_error("%d candidate blocks exceed the per-head select limit %d", n_cand, kMaxStreamCand);
     return LKV_ERR_UNSUPPORTED;
   }
   if (sorted && k > kMaxSortedK) {
@@ -475,8 +676,13 @@ extern "C" int lkv_bound_topk(uintptr_t stream, const void* q, int q_dtype, cons
                                                            cand_offset, n_cand, rank_mode, bounds, bstride);
   }
   if (rc != LKV_OK || k == 0) return rc;
-  hipLaunchKernelGGL(select_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k, cand_offset,
-                     sorted, out_idx, idx_stride);
+  if (n_cand <= kMaxCand) {
+    hipLaunchKernelGGL(select_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k, cand_offset,
+                       sorted, out_idx, idx_stride);
+  } else {
+    hipLaunchKernelGGL(select_stream_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k,
+                       cand_offset, sorted, out_idx, idx_stride);
+  }
   LKV_CHECK_LAUNCH("select");
   return LKV_OK;
 }

@@ -12,7 +12,8 @@ Workloads (32 query / 8 KV heads, 16-token blocks, lazy sealing: fill 16, candid
 * 1B-shaped, 65,536 tokens, d 64, float16, K 1,024, sealed blocks as int8 records (HBM or host);
 * 8B-shaped, 131,072 tokens, d 128, bfloat16, K 512, read zero-copy from mapped host memory;
 * 8B-shaped, 131,072 tokens, d 128, bfloat16, exact split: K of 512 / 2,048 / 4,096 selected
-  from HBM, every other sealed block from the int8 host tier, merged by LSE.
+  from HBM, every other sealed block from the int8 host tier, merged by LSE;
+* 8B-shaped, 524,288 tokens (32,766 candidates per head: the streaming select), K 2,048, zero-copy.
 """
 
 from __future__ import annotations
@@ -218,3 +219,19 @@ def test_exact_split_128k_bfloat16(exact_layer, k: int) -> None:  # noqa: ANN001
     dev_o, dev_l = np.abs(out - dense_o).max(), np.abs(lse - dense_l).max()
     print(f"exact split K={k}: max|out - dense| {dev_o:.2e}, max|lse - dense| {dev_l:.2e}")
     assert dev_o < 5e-2 and dev_l < 5e-2
+
+
+def test_zero_copy_decode_512k_streams_the_selection() -> None:
+    """A context past the register-resident select (32,766 candidates per head): 524,288 tokens,
+    bf16 d128, K 2,048, read zero-copy."""
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+
+    layer = _Layer(128, 524288, torch.bfloat16, int8=False, meta_from="exact")
+    host = pinned_empty(tuple(layer.pool.shape), torch.bfloat16)
+    host.copy_(layer.pool)
+    idx = layer.select(2048)
+    out, lse = _decode(layer, idx, kernels.pool_source(host))
+    want_o, want_l = layer.oracle(idx.cpu().numpy(), exact_remainder=False)
+    assert np.abs(out - want_o).max() < TOL
+    assert np.abs(lse - want_l).max() < TOL

@@ -181,6 +181,31 @@ def test_top_blocks_selects_the_oracle_set(h: int, n: int, d: int, g: int, k: in
         assert (np.diff(b) <= 0).all()
 
 
+@pytest.mark.parametrize(("h", "n", "d", "k", "sorted_"), [(8, 12289, 128, 512, False), (4, 40000, 64, 2048, True), (2, 100000, 64, 4096, False), (1, 70000, 128, 17, True)])
+def test_long_context_selection_streams_the_bounds(h: int, n: int, d: int, k: int, sorted_: bool) -> None:
+    """More candidates per head than the registers hold: the streaming select gives the oracle's set."""
+    from lazykv_amd import selection
+
+    q, kmin, kmax = _meta_case(n + k, h, n, 16, d, 4, torch.bfloat16)
+    want = R.quest_bound(_f64(q), _f64(kmin), _f64(kmax))
+    err = _abs_err(_f64(q), _f64(kmin), _f64(kmax))
+    from lazykv_amd import kernels
+
+    full_min = torch.cat([torch.zeros((h, 1, d), dtype=torch.bfloat16), kmin], dim=1)[None].cuda()
+    full_max = torch.cat([torch.zeros((h, 1, d), dtype=torch.bfloat16), kmax], dim=1)[None].cuda()
+    idx = kernels.bound_topk(q.cuda(), full_min, full_max, k, cand_offset=1, n_cand=n, sorted_=sorted_)
+    got = idx.cpu().numpy() - 1
+    for j in range(h):
+        assert R.selection_ok(got[j], want[j], k, abs_err=err)[0], j
+        assert len(set(got[j].tolist())) == k
+        if not sorted_:
+            assert (np.diff(got[j]) > 0).all()
+    if sorted_:
+        b = selection.quest_bound(q.view(1, -1, 1, d).cuda(), full_min, full_max, torch.float32)[0].cpu().numpy()
+        for j in range(h):
+            assert (np.diff(b[j][got[j] + 1]) <= 0).all()
+
+
 def test_unsorted_selection_is_ascending_and_offset() -> None:
     from lazykv_amd import kernels
 
