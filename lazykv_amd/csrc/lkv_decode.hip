@@ -28,8 +28,11 @@
 
 namespace {
 
+// Workgroup shapes: 4 waves when the launch reads host memory (its grid is sized by the host
+// budget), 8 waves when everything is in HBM (about one workgroup per CU; see make_plan).
 constexpr int kThreads = 256;
-constexpr int kWaves = 4;
+constexpr int kWaves = kThreads / 64;
+constexpr int kThreadsHbm = 512;
 constexpr int kMaxSplits = 512;  // partials per KV head
 
 struct Src {
@@ -65,6 +68,7 @@ struct DecodeArgs {
   const int32_t* loc;
   int64_t loc_stride;
   Src slots;
+  int nt;  // workgroup size the plan chose (kThreads or kThreadsHbm)
 };
 
 constexpr int32_t kLocMiss = 0x40000000;
@@ -377,8 +381,9 @@ __device__ __forceinline__ void attend_fill(const DecodeArgs& a, int block, int 
   }
 }
 
-template <int D, int MT, int G>
-__global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
+template <int D, int MT, int G, int NT>
+__global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
+  constexpr int NW = NT / 64;
   constexpr int EPL = D / 16;
   const int h = blockIdx.x % a.n_kv;
   const int split = blockIdx.x / a.n_kv;
@@ -386,8 +391,8 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
   const int r = lane >> 4, c = lane & 15;
   const int S = a.splits_a + a.splits_b;
 
-  __shared__ float s_m[kWaves][G], s_l[kWaves][G];
-  __shared__ float s_o[kWaves][G][D];
+  __shared__ float s_m[NW][G], s_l[NW][G];
+  __shared__ float s_o[NW][G][D];
   __shared__ uint32_t s_excl[64];  // segment B: bitmap of excluded blocks in this run
 
   float q[G][EPL];
@@ -413,14 +418,14 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
     const int has_sink = a.sink_block >= 0;
     const int n_sel = a.attend_selected ? a.k : 0;
     if (has_sink && first == 0 && wave == 0) attend_two<D, MT, G>(a, a.sink, a.sink_block, -1, h, a.bs, q, r, c, st);
-    if (a.cur_block >= 0 && last == a.n_a && wave == kWaves - 1)
+    if (a.cur_block >= 0 && last == a.n_a && wave == NW - 1)
       attend_two<D, MT, G>(a, a.cur, a.cur_block, -1, h, a.fill, q, r, c, st);
     // Selected items of this run: idx positions [js, je), two per wave per round.
     const int js = max(first, has_sink) - has_sink;
     const int je = min(last, has_sink + n_sel) - has_sink;
     const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
     static_assert(kPairs<G> == 1, "the hybrid path below attends one pair per wave per round");
-    for (int j = js + wave; j < je; j += kPairs<G> * kWaves) {
+    for (int j = js + wave; j < je; j += kPairs<G> * NW) {
       const int b0 = idx_h[j];
       if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
         const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
@@ -431,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
         }
         continue;
       }
-      const int b1 = (kPairs<G> == 2 && j + kWaves < je) ? idx_h[j + kWaves] : -1;
+      const int b1 = (kPairs<G> == 2 && j + NW < je) ? idx_h[j + NW] : -1;
       attend_two<D, MT, G>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
     }
   } else {
@@ -439,14 +444,14 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
     const int sb = split - a.splits_a;
     const int lo = a.rem_first + sb * a.per_b;
     const int hi = min(a.rem_last, lo + a.per_b);
-    for (int i = threadIdx.x; i < 64; i += kThreads) s_excl[i] = 0;
+    for (int i = threadIdx.x; i < 64; i += NT) s_excl[i] = 0;
     __syncthreads();
     const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
     // Eight index loads in flight per thread per round.
-    for (int i0 = threadIdx.x; i0 < a.k; i0 += 8 * kThreads) {
+    for (int i0 = threadIdx.x; i0 < a.k; i0 += 8 * NT) {
       int bv[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) bv[u] = i0 + u * kThreads < a.k ? idx_h[i0 + u * kThreads] : -1;
+      for (int u = 0; u < 8; ++u) bv[u] = i0 + u * NT < a.k ? idx_h[i0 + u * NT] : -1;
 #pragma unroll
       for (int u = 0; u < 8; ++u)
         if (bv[u] >= lo && bv[u] < hi) atomicOr(&s_excl[(bv[u] - lo) >> 5], 1u << ((bv[u] - lo) & 31));
@@ -458,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
       int have = 0;
       while (have < kPairs<G> && b < hi) {
         if (!((s_excl[(b - lo) >> 5] >> ((b - lo) & 31)) & 1u)) pick[have++] = b;
-        b += kWaves;
+        b += NW;
       }
       if (have) attend_two<D, MT, G>(a, a.rem, pick[0], pick[1], h, a.bs, q, r, c, st);
     }
@@ -482,15 +487,15 @@ __global__ __launch_bounds__(kThreads) void sparse_decode_kernel(DecodeArgs a) {
   __syncthreads();
   float* pml = a.part_ml + ((int64_t)h * S + split) * G * 2;
   float* po = a.part_o + ((int64_t)h * S + split) * G * D;
-  for (int t = threadIdx.x; t < G * D; t += kThreads) {
+  for (int t = threadIdx.x; t < G * D; t += NT) {
     const int j = t / D, dd = t % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][j]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][j]);
     float O = 0.0f, L = 0.0f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < NW; ++w) {
         const float wt = exp2f(s_m[w][j] - M);
         O += s_o[w][j][dd] * wt;
         L += s_l[w][j] * wt;
@@ -586,6 +591,7 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restri
 
 struct Plan {
   int n_a, per_a, splits_a, per_b, splits_b;
+  int nt = kThreads;  // workgroup size of the launch
 };
 
 // Where the selected and remainder blocks live, and the bytes of one of their pairs.
@@ -609,7 +615,7 @@ static int host_splits(size_t pair_bytes, int n_kv, double budget) {
 // partial count per head stays within kMaxSplits. A segment read from host memory is then cut
 // into fewer runs (host_splits); that never raises the partial count, so the workspace sized by
 // the plan without hints covers every plan.
-static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHints()) {
+static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHints(), int cus = 0) {
   Plan p;
   p.n_a = (d->sink_block >= 0 ? 1 : 0) + (d->attend_selected ? d->k : 0) + (d->cur_block >= 0 ? 1 : 0);
   // At least 8 items (two pairs per wave), and at most 64 partials per head so that the merge
@@ -623,6 +629,17 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
   if (p.per_b > 2048) p.per_b = 2048;  // the exclusion bitmap holds 2048 blocks
   p.splits_b = n_b > 0 ? (n_b + p.per_b - 1) / p.per_b : 0;
   const int n_sel = d->attend_selected ? d->k : 0;
+  if (cus > 0 && !hint.sel_host && !hint.rem_host && d->n_q / d->n_kv <= 4) {
+    // Everything in HBM: 8-wave workgroups, about one per CU for the gathered set (measured at
+    // the 8B shape: 17.8 us against 20.2 us for 58 four-wave workgroups per head, which leave a
+    // tail of CUs with two), at least one pair per wave. (Groups of 8 query heads need more
+    // registers than an 8-wave workgroup leaves a wave, and keep the 4-wave shape.)
+    p.nt = kThreadsHbm;
+    const int per_head = cus / d->n_kv > 1 ? cus / d->n_kv : 1;
+    p.per_a = (p.n_a + per_head - 1) / per_head;
+    if (p.per_a < kThreadsHbm / 64) p.per_a = kThreadsHbm / 64;
+    p.splits_a = p.n_a > 0 ? (p.n_a + p.per_a - 1) / p.per_a : 0;
+  }
   if (hint.sel_host && n_sel > 0) {
     const int s = host_splits(hint.sel_pair, d->n_kv, lkv_host_read_inflight());
     if (s < p.splits_a) {
@@ -644,7 +661,16 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
 template <int D, int MT, int G>
 int launch(hipStream_t stream, DecodeArgs& a) {
   const int S = a.splits_a + a.splits_b;
-  hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G>), dim3(S * a.n_kv), dim3(kThreads), 0, stream, a);
+  bool launched = false;
+  if constexpr (G <= 4) {
+    if (a.nt == kThreadsHbm) {
+      hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
+      launched = true;
+    }
+  }
+  if (!launched) {
+    hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreads>), dim3(S * a.n_kv), dim3(kThreads), 0, stream, a);
+  }
   LKV_CHECK_LAUNCH("sparse_decode");
   hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(512), 0, stream, a.part_ml, a.part_o, S,
                      a.out, a.out_dtype, a.lse);
@@ -767,6 +793,18 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   }
 }
 
+// Compute units of the current device, cached per device.
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int v = 0;
+    cached[dev] = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+  }
+  return cached[dev];
+}
+
 static Src to_src(const lkv_kv_source* s) {
   Src o{};
   if (s) {
@@ -798,8 +836,10 @@ static int check_src(const lkv_kv_source* s, const char* name, int model_dtype, 
 
 extern "C" size_t lkv_sparse_decode_workspace_bytes(const lkv_decode_desc* d) {
   if (d == nullptr || d->n_kv <= 0 || d->n_q <= 0 || d->n_q % d->n_kv) return 0;
+  // Host plans only cut the default plan's partial count; the HBM plan may raise it.
   const Plan p = make_plan(d);
-  const size_t S = (size_t)(p.splits_a + p.splits_b);
+  const Plan ph = make_plan(d, PlanHints(), device_cus());
+  const size_t S = (size_t)max(p.splits_a + p.splits_b, ph.splits_a + ph.splits_b);
   const size_t G = (size_t)(d->n_q / d->n_kv);
   return lkv_align_up((size_t)d->n_kv * S * G * 2 * 4, 256) + lkv_align_up((size_t)d->n_kv * S * G * d->head_dim * 4, 256);
 }
@@ -871,7 +911,7 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
     hint.rem_host = (rem->flags & LKV_SRC_HOST) != 0;
     hint.rem_pair = lkv_pair_bytes(rem, d.block_size, d.head_dim);
   }
-  const Plan p = make_plan(desc, hint);
+  const Plan p = make_plan(desc, hint, device_cus());
   const int S = p.splits_a + p.splits_b;
   LKV_CHECK_ARG(S > 0, "nothing to attend");
   LKV_CHECK_ARG(S <= kMaxSplits, "too many partials (%d)", S);
@@ -902,6 +942,7 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
   a.splits_a = p.splits_a;
   a.per_b = p.per_b;
   a.splits_b = p.splits_b;
+  a.nt = p.nt;
   a.out = out;
   a.out_dtype = out_dtype;
   a.lse = lse;
