@@ -257,3 +257,29 @@ def test_graph_replays_equal_the_eager_step() -> None:
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(idx, ref_i) and torch.equal(out, ref_o) and torch.equal(lse, ref_l), i
+
+
+@pytest.mark.parametrize("fetch", ["zerocopy", "hybrid", "resident"])
+def test_decode_steps_never_synchronise_with_the_host(fetch: str) -> None:
+    """Selection, decode, append and seal run with torch's sync debug mode set to raise: no step
+    waits on the GPU from the host (the reference's rank() copies ids to the host, :387)."""
+    from lazykv_amd.tiered import TieredCache
+
+    keys, values, gen = _prompt(8, 700)  # 43 full blocks + 12 tokens: a seal within 4 steps
+    cache = TieredCache([(keys.cuda(), values.cuda())] * 2, 8, BS, 1024, dense_layers=0, fetch=fetch)
+    q = torch.randn((1, H * G, 1, D), generator=gen).to(torch.bfloat16).cuda()
+    kv = torch.randn((1, H, 1, D), generator=gen).to(torch.bfloat16).cuda()
+    seals = cache.counters.seals
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        for _ in range(6):
+            for layer in (0, 1):
+                cache.update(kv, kv, layer)
+                decoded = cache.select(layer, q, scaling=D**-0.5)
+                assert decoded is not None
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    assert cache.counters.seals > seals
+    assert torch.isfinite(decoded.out.float()).all()
