@@ -145,10 +145,11 @@ int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void*
  * them with -1 once. Each call first updates the tables for the selection idx: with as many slots
  * as selected blocks, the slots the selection does not hit are exactly the victims, taken in
  * ascending slot order by the missed blocks in ascending block order. It then attends as
- * lkv_sparse_decode does over `host` (mapped host memory, model dtype): a hit is read from its slot
- * in HBM; a miss is read from `host` and its pair copied into its new slot on the way. The output
- * and LSE equal lkv_sparse_decode's over `host` bit for bit; only where the bytes come from
- * differs. desc->k <= 4096, no remainder. */
+ * lkv_sparse_decode does over `host` (mapped host memory: model-dtype pairs, or int8 records as in
+ * rung 8, lazykv/tiered.py:182-196): a hit is read from its slot in HBM; a miss is read from `host`
+ * and its pair -- for int8 records, the dequantised model-dtype rows -- written into its new slot on
+ * the way. `slots` holds the model dtype. The output and LSE equal lkv_sparse_decode's over `host`
+ * bit for bit; only where the bytes come from differs. desc->k <= 4096, no remainder. */
 size_t lkv_hybrid_decode_workspace_bytes(const lkv_decode_desc* desc);
 int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
                       const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* idx, int64_t idx_stride,

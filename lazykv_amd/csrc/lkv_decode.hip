@@ -365,8 +365,8 @@ __device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, in
 }
 
 // A residency miss: attend `block` of the host source exactly as attend_two does, and copy each
-// chunk it loads into `slot` of the slot pool. Model-dtype sources only (the slots hold the model
-// dtype); the same loads and arithmetic as the zero-copy path, so the result is identical.
+// chunk it loads into `slot` of the slot pool (model-dtype sources; int8 records take
+// attend_fill_i8). The same loads and arithmetic as the zero-copy path, so the result is identical.
 template <int D, int MT, int G>
 __device__ __forceinline__ void attend_fill(const DecodeArgs& a, int block, int slot, int h, const float (&q)[G][D / 16],
                                             int r, int c, WaveState<D, G>& st) {
@@ -378,6 +378,44 @@ __device__ __forceinline__ void attend_fill(const DecodeArgs& a, int block, int 
     load_raw<D, MT>(a.sel, block, h, t0, nit, a.bs, r, c, raw);
     store_raw<D, MT>(a.slots, slot, h, t0, nit, r, c, raw);
     consume_chunk<D, G>(q, Widen<D, MT>(raw), raw, t0, nit, a.bs, r, st);
+  }
+}
+
+// A residency miss on an int8 host tier: the record is dequantised in registers as the zero-copy
+// path does, its rows -- model-dtype values -- are written into `slot`, and the chunk is attended.
+// A later hit reads back exactly these values, so hits and misses attend the same numbers.
+template <int D, int MT, int G>
+__device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, int slot, int h, const float (&q)[G][D / 16],
+                                               int r, int c, WaveState<D, G>& st) {
+  using T = typename lkv::Elem<MT>::T;
+  constexpr int EPL = D / 16;
+  if (block < 0 || (int64_t)block >= a.sel.nblk || slot < 0 || (int64_t)slot >= a.slots.nblk) return;  // wave-uniform
+  const int64_t off = (int64_t)slot * a.slots.bstride + (int64_t)h * a.slots.hstride + c * EPL;
+  T* kb = (T*)a.slots.k + off;
+  T* vb = (T*)a.slots.v + off;
+#pragma unroll 1
+  for (int t0 = 0; t0 < a.bs; t0 += 16) {
+    const int nit = min(4, (a.bs - t0) >> 2);
+    RawI8<D> raw;
+    load_raw<D>(a.sel, a.bs, block, h, t0, nit, a.bs, r, c, raw);
+    const WidenI8<D, MT> wd(raw);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < nit) {
+        const int row = t0 + r + 4 * i;
+        float x[EPL];
+        T t[EPL];
+        wd.key(raw, i, x);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) t[e] = lkv::Elem<MT>::store(x[e]);
+        __builtin_memcpy(kb + (int64_t)row * D, t, sizeof(t));
+        wd.value(raw, i, x);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) t[e] = lkv::Elem<MT>::store(x[e]);
+        __builtin_memcpy(vb + (int64_t)row * D, t, sizeof(t));
+      }
+    }
+    consume_chunk<D, G>(q, wd, raw, t0, nit, a.bs, r, st);
   }
 }
 
@@ -430,7 +468,11 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
         const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
         if (l >= 0 && (l & kLocMiss)) {
-          attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
+          if (a.sel.dtype == LKV_INT8_RECORD) {
+            attend_fill_i8<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
+          } else {
+            attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
+          }
         } else if (l >= 0) {
           attend_two<D, MT, G>(a, a.slots, l, -1, h, a.bs, q, r, c, st);
         }
@@ -997,8 +1039,11 @@ extern "C" int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, 
   LKV_CHECK_ARG(d.rem_last == d.rem_first, "hybrid decode has no remainder");
   LKV_CHECK_ARG(d.k <= kMaxSlots, "k=%d exceeds the hybrid slot limit %d", d.k, kMaxSlots);
   LKV_CHECK_ARG(d.n_kv > 0 && idx_stride >= d.k, "bad n_kv or idx_stride");
-  LKV_CHECK_ARG(lkv_is_model_dtype(host->dtype) && host->v != nullptr, "the hybrid host pool holds model-dtype pairs");
-  LKV_CHECK_ARG(slots->dtype == host->dtype && slots->k != nullptr && slots->v != nullptr, "slots must match the host pool's dtype");
+  const int model = host->dtype == LKV_INT8_RECORD ? host->deq_dtype : host->dtype;
+  LKV_CHECK_ARG(host->dtype == LKV_INT8_RECORD || (lkv_is_model_dtype(host->dtype) && host->v != nullptr),
+                "the hybrid host pool holds model-dtype pairs or int8 records");
+  LKV_CHECK_ARG(slots->dtype == model && lkv_is_model_dtype(model) && slots->k != nullptr && slots->v != nullptr,
+                "slots must hold the model dtype (the host pool's, or its records' dequantised dtype)");
   LKV_CHECK_ARG(slots->n_blocks == d.k, "the slot pool holds k=%d slots per head, got %lld", d.k, (long long)slots->n_blocks);
   LKV_CHECK_ARG(block_slot != nullptr && slot_block != nullptr, "residency tables missing");
   LKV_CHECK_ARG(block_slot_stride >= host->n_blocks && slot_block_stride >= d.k, "residency table strides too small");

@@ -186,8 +186,6 @@ class TieredLayer:
         if fetch == "hybrid":
             if n_slots not in (None, k_blocks):
                 raise ValueError(f"the hybrid tier keeps one HBM slot per selected block: n_slots must be k_blocks={k_blocks}")
-            if quant is not None:
-                raise ValueError("the hybrid tier's slots hold the model dtype: an int8 host tier needs fetch='zerocopy'")
         elif n_slots not in (None, 0):
             raise ValueError("the GPU tier holds only the sink and the current block in slots (n_slots=0)")
         if quant not in (None, "int8"):

@@ -1,6 +1,7 @@
 """Device-side hybrid residency on the GPU: over a drifting sequence of decode steps, the hybrid
 decode's output and LSE equal the zero-copy decode's bit for bit, its residency tables equal the
-oracle's (oracle.reference.residency_step), and every slot holds an exact copy of its block."""
+oracle's (oracle.reference.residency_step), and every slot holds an exact copy of its block (for
+an int8 host tier: the block's dequantised rows, as lkv_unpack_int8 writes them)."""
 
 from __future__ import annotations
 
@@ -28,17 +29,34 @@ def _layer(seed: int, h: int, g: int, n: int, bs: int, d: int, dt: torch.dtype):
     return w, pool, host, kmin, kmax
 
 
-@pytest.mark.parametrize(("h", "g", "n", "bs", "d", "k", "dt", "fill"), [(8, 4, 300, 16, 128, 32, torch.bfloat16, 16), (4, 4, 200, 16, 64, 24, torch.float16, 5), (2, 8, 150, 32, 128, 40, torch.bfloat16, 19)])
-def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, fill: int) -> None:
+@pytest.mark.parametrize(
+    ("h", "g", "n", "bs", "d", "k", "dt", "fill", "quant"),
+    [
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, 16, None),
+        (4, 4, 200, 16, 64, 24, torch.float16, 5, None),
+        (2, 8, 150, 32, 128, 40, torch.bfloat16, 19, None),
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, 16, "int8"),
+        (4, 4, 200, 16, 64, 24, torch.float16, 5, "int8"),
+    ],
+)
+def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, fill: int, quant: str | None) -> None:
     from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
 
     w, pool, host, kmin, kmax = _layer(n + k, h, g, n, bs, d, dt)
+    hsrc = kernels.pool_source(host)
+    expect = pool  # what each slot must hold: the block's rows as a decode reads them
+    if quant == "int8":
+        recs = kernels.pack_int8(pool.reshape(n * h, 2, bs, d))
+        expect = kernels.unpack_int8(recs, bs, d, dt).reshape(n, h, 2, bs, d)
+        host = pinned_empty((n, h, recs.shape[1]), torch.uint8)
+        host.copy_(recs.reshape(n, h, -1))
+        hsrc = kernels.record_source(host, dt)
     res = kernels.Residency.allocate(k, h, n, bs, d, dt, torch.device("cuda"))
     bs_ref = np.full((h, n), -1, dtype=np.int64)
     sb_ref = np.full((h, k), -1, dtype=np.int64)
     slots_src = pool[[0, n - 1]].contiguous()
     ss = kernels.pool_source(slots_src)
-    hsrc = kernels.pool_source(host)
     gen = torch.Generator().manual_seed(5)
     q0 = w.query.float()
     hits = 0
@@ -58,7 +76,7 @@ def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, 
         hits += int((np.take_along_axis(prev, chosen, axis=1) >= 0).sum())
         # every slot holds an exact copy of the block the table names
         for j in range(h):
-            assert torch.equal(res.slots[:, j], pool[torch.from_numpy(sb_ref[j]).cuda(), j])
+            assert torch.equal(res.slots[:, j], expect[torch.from_numpy(sb_ref[j]).cuda(), j])
     assert hits > 0  # the drift keeps part of each selection resident
 
 

@@ -122,7 +122,7 @@ def test_boundary_stores_every_full_block_with_exact_metadata() -> None:
     assert layer.host_bytes() == 62 * H * 2 * BS * D * 2
 
 
-@pytest.mark.parametrize(("fetch", "quant"), [("zerocopy", None), ("zerocopy", "int8"), ("resident", None), ("hybrid", None)])
+@pytest.mark.parametrize(("fetch", "quant"), [("zerocopy", None), ("zerocopy", "int8"), ("resident", None), ("hybrid", None), ("hybrid", "int8")])
 def test_decode_through_seals_matches_the_oracle(fetch: str, quant: str | None) -> None:
     """Each step appends a token (sealing every 16), ranks and decodes; every step is checked."""
     from lazykv_amd.tiered import TieredLayer
