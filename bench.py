@@ -24,7 +24,8 @@ Other workloads (same JSON contract, for the parity-test configurations):
                 layer's KV turned into the int8 host tier by the fused pack + metadata kernel
   hybrid128k -- the 8B-shaped step over a sequence of decode steps whose queries drift (`--drift`):
                 hybrid residency (HBM slots for the k most recently selected blocks per head, misses
-                read in place and admitted) against the zero-copy read of the same sequence
+                read in place and admitted) against the zero-copy read of the same sequence; the host
+                tier holds bf16 pairs or, with `--quant int8`, int8 records
 
     python bench.py [--workload W] [--steps K] [--warmup W] [--layers L] [--no-cpu-baseline]
 """
@@ -79,6 +80,7 @@ def main() -> int:
     p.add_argument("--coherent", action="store_true", help="fine-grained (device-uncached) host pools")
     p.add_argument("--drift", type=float, default=0.25, help="hybrid128k: per-step query drift (relative to the query's RMS)")
     p.add_argument("--seq", type=int, default=16, help="hybrid128k: decode steps in the sequence")
+    p.add_argument("--quant", choices=["none", "int8"], default="none", help="hybrid128k: host tier as model-dtype pairs or int8 records")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path has no multi-GPU mode (asked for --gpus {args.gpus}).", file=sys.stderr)
@@ -491,6 +493,7 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
 
     from lazykv_amd import kernels
     from lazykv_amd.pinned import pinned_empty
+    from lazykv_amd.quant import packed_pair_bytes
     from lazykv_amd.workload import draw_layer, to_pool
 
     dev = torch.device("cuda", 0)
@@ -500,6 +503,7 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
     N = T // BS
     n_sealed, fill, n_cand = N - 1, BS, N - 2
     S = max(2, args.seq)
+    int8 = args.quant == "int8"
     t0 = time.time()
     layers = []
     for li in range(L):
@@ -507,10 +511,17 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
         pool = to_pool(w.keys, w.values, BS)
         kmin = torch.zeros((1, H, N, d), dtype=dtype, device=dev)
         kmax = torch.zeros_like(kmin)
-        kernels.store_blocks(kernels.dense_source(w.keys, w.values, BS), n_kv=H, head_dim=d, block_size=BS, first_block=0, n_blocks=n_sealed, kmin=kmin, kmax=kmax)
-        host = pinned_empty(tuple(pool.shape), dtype)
-        host.copy_(pool)
-        layers.append({"q": w.query.float(), "kmin": kmin, "kmax": kmax, "slots": pool[[0, N - 1]].contiguous(), "host": host,
+        dense = kernels.dense_source(w.keys, w.values, BS)
+        if int8:  # records packed into the host pool; metadata over the dequantised keys
+            host = pinned_empty((N, H, packed_pair_bytes(BS, d)), torch.uint8)
+            hs = kernels.record_source(host, dtype)
+            kernels.store_blocks(dense, dst=hs, n_kv=H, head_dim=d, block_size=BS, first_block=0, n_blocks=n_sealed, kmin=kmin, kmax=kmax)
+        else:
+            kernels.store_blocks(dense, n_kv=H, head_dim=d, block_size=BS, first_block=0, n_blocks=n_sealed, kmin=kmin, kmax=kmax)
+            host = pinned_empty(tuple(pool.shape), dtype)
+            host.copy_(pool)
+            hs = kernels.pool_source(host)
+        layers.append({"q": w.query.float(), "kmin": kmin, "kmax": kmax, "slots": pool[[0, N - 1]].contiguous(), "host": host, "hs": hs,
                        "res": kernels.Residency.allocate(k, H, N, BS, d, dtype, dev)})
         del w, pool
     # The query sequence: each step's query is the layer's base query plus a fresh drift.
@@ -532,7 +543,7 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
     rank_h, rank_z, dec_h, dec_z = [], [], [], []
     for li, st in enumerate(layers):
         ss = kernels.pool_source(st["slots"])
-        hs = kernels.pool_source(st["host"])
+        hs = st["hs"]
         common = dict(n_kv=H, block_size=BS, scale=d**-0.5, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=fill)
         rank_h.append(kernels.PreparedBoundTopk(q_static[li], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx_h[li], ws=ws_sel))
         rank_z.append(kernels.PreparedBoundTopk(q_static[li], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx_z[li], ws=ws_sel))
@@ -575,7 +586,7 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
     hit_rate = float(hits.mean())
     warm_h = statistics.mean(t_h[1:])
     warm_z = statistics.mean(t_z[1:])
-    pair = 2 * BS * d * torch.tensor([], dtype=dtype).element_size()
+    pair = packed_pair_bytes(BS, d) if int8 else 2 * BS * d * torch.tensor([], dtype=dtype).element_size()
     miss_bytes = (1.0 - hit_rate) * H * k * pair
     log(f"hybrid128k: hybrid {warm_h:.1f} us/layer (cold step {t_h[0]:.1f}), zero-copy {warm_z:.1f} us/layer, hit rate {hit_rate:.3f}")
     return {
@@ -583,9 +594,11 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
         "value": round(warm_h, 3), "unit": "us/layer", "n_gpus": 1, "steps": S - 1, "warmup": 1,
         "ms_per_step": round(warm_h * L / 1e3, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16" if dtype == torch.bfloat16 else "f16", "data": "synthetic",
-        "config": {"workload": f"Llama-3.1-8B-shaped tiered decode, {L} layers, {T} tokens, K={k} of {n_cand} per KV head, bf16 KV in mapped host memory, "
+        "config": {"workload": f"Llama-3.1-8B-shaped tiered decode, {L} layers, {T} tokens, K={k} of {n_cand} per KV head, "
+                               f"{'int8 records' if int8 else 'bf16 KV'} in mapped host memory, "
                                f"{k} HBM slots per head; {S} steps whose queries are the layer's query plus N(0, {args.drift}^2 * rms^2) drift",
-                   "layers": L, "tokens": T, "q_heads": N_Q, "kv_heads": H, "head_dim": d, "block_size": BS, "k": k, "drift": args.drift, "sequence_steps": S},
+                   "layers": L, "tokens": T, "q_heads": N_Q, "kv_heads": H, "head_dim": d, "block_size": BS, "k": k, "drift": args.drift, "sequence_steps": S,
+                   "host_tier": "int8" if int8 else "bf16"},
         "hybrid_us_per_layer": round(warm_h, 2), "hybrid_cold_step_us_per_layer": round(t_h[0], 2),
         "zerocopy_us_per_layer": round(warm_z, 2), "speedup_vs_zerocopy": round(warm_z / warm_h, 4),
         "hit_rate": round(hit_rate, 4), "pcie_bytes_per_layer": int(miss_bytes),

@@ -178,14 +178,26 @@ __device__ __forceinline__ void load_raw(const Src& s, int bs, int block, int h,
   const uint16_t* scales = (const uint16_t*)(rec + 2 * bs * D);
   load_words(scales + c * EPL, raw.ks);
   load_words(scales + D + c * EPL, raw.kz);
+  // The chunk's value scales and zeros in one 64-byte read: lane c < 8 of each row group loads
+  // the float16 pair vs[t0 + 2c, +1], lane c >= 8 the pair vz[t0 + 2(c - 8), +1] (pairs past the
+  // record's bs rows are not read). Each row's pair is then taken from the lane holding it.
+  const int m = c & 7;
+  const uint32_t sz = t0 + 2 * m + 2 <= bs ? *(const uint32_t*)(scales + 2 * D + (c >> 3) * bs + t0 + 2 * m) : 0u;
+  uint32_t wvs[4], wvz[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // every lane takes part in the shuffles
+    const int local = r + 4 * i;
+    wvs[i] = (uint32_t)__shfl((int)sz, (r << 4) + (local >> 1));
+    wvz[i] = (uint32_t)__shfl((int)sz, (r << 4) + 8 + (local >> 1));
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = t0 + r + 4 * i;
     if (i < nit && row < limit) {
       load_words(rec + row * D + c * EPL, raw.k[i]);
       load_words(rec + bs * D + row * D + c * EPL, raw.v[i]);
-      raw.vs[i] = scales[2 * D + row];
-      raw.vz[i] = scales[2 * D + bs + row];
+      raw.vs[i] = (row & 1) ? wvs[i] >> 16 : wvs[i] & 0xffffu;
+      raw.vz[i] = (row & 1) ? wvz[i] >> 16 : wvz[i] & 0xffffu;
     } else {
 #pragma unroll
       for (int w = 0; w < RawI8<D>::W; ++w) raw.k[i][w] = raw.v[i][w] = 0u;
