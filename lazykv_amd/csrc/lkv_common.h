@@ -143,44 +143,62 @@ __device__ __forceinline__ void store_any(void* p, int64_t i, int dt, float v) {
   }
 }
 
+// The 32-bit words of N contiguous elements (N * sizeof(T) bytes, naturally aligned, a whole
+// number of words), loaded as the widest vectors that fit; kept raw so that a caller can issue
+// several loads before it widens any of them.
+template <int DT, int N>
+struct RowWords {
+  static constexpr int BYTES = N * (int)sizeof(typename Elem<DT>::T);
+  static_assert(BYTES % 4 == 0, "segment must be dword sized");
+  static constexpr int WORDS = BYTES / 4;
+  uint32_t w[WORDS];
+};
+
+template <int DT, int N>
+__device__ __forceinline__ void load_row_words(const typename Elem<DT>::T* p, RowWords<DT, N>& r) {
+  constexpr int WORDS = RowWords<DT, N>::WORDS;
+  if constexpr (WORDS % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < WORDS / 4; ++i) {
+      uint4 v = ((const uint4*)p)[i];
+      r.w[4 * i + 0] = v.x;
+      r.w[4 * i + 1] = v.y;
+      r.w[4 * i + 2] = v.z;
+      r.w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (WORDS == 2) {
+    uint2 v = *(const uint2*)p;
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < WORDS; ++i) r.w[i] = ((const uint32_t*)p)[i];
+  }
+}
+
+template <int DT, int N>
+__device__ __forceinline__ void widen_row_words(const RowWords<DT, N>& r, float (&out)[N]) {
+  if constexpr (sizeof(typename Elem<DT>::T) == 4) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = bits_to_float(r.w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      out[2 * i] = Elem<DT>::load((uint16_t)(r.w[i] & 0xffffu));
+      out[2 * i + 1] = Elem<DT>::load((uint16_t)(r.w[i] >> 16));
+    }
+  }
+}
+
 // Load N contiguous elements (N * sizeof(T) bytes, naturally aligned) and widen to float.
 template <int DT, int N>
 __device__ __forceinline__ void load_row_segment(const typename Elem<DT>::T* p, float (&out)[N]) {
-  using T = typename Elem<DT>::T;
-  constexpr int BYTES = N * (int)sizeof(T);
-  static_assert(BYTES % 4 == 0 || BYTES == 2, "segment must be dword sized");
-  if constexpr (BYTES == 2) {
+  if constexpr (N * sizeof(typename Elem<DT>::T) == 2) {
     out[0] = Elem<DT>::load(p[0]);
   } else {
-    constexpr int WORDS = BYTES / 4;
-    uint32_t w[WORDS];
-    if constexpr (WORDS % 4 == 0) {
-#pragma unroll
-      for (int i = 0; i < WORDS / 4; ++i) {
-        uint4 v = ((const uint4*)p)[i];
-        w[4 * i + 0] = v.x;
-        w[4 * i + 1] = v.y;
-        w[4 * i + 2] = v.z;
-        w[4 * i + 3] = v.w;
-      }
-    } else if constexpr (WORDS == 2) {
-      uint2 v = *(const uint2*)p;
-      w[0] = v.x;
-      w[1] = v.y;
-    } else {
-#pragma unroll
-      for (int i = 0; i < WORDS; ++i) w[i] = ((const uint32_t*)p)[i];
-    }
-    if constexpr (sizeof(T) == 4) {
-#pragma unroll
-      for (int i = 0; i < N; ++i) out[i] = bits_to_float(w[i]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < N / 2; ++i) {
-        out[2 * i] = Elem<DT>::load((uint16_t)(w[i] & 0xffffu));
-        out[2 * i + 1] = Elem<DT>::load((uint16_t)(w[i] >> 16));
-      }
-    }
+    RowWords<DT, N> r;
+    load_row_words<DT, N>(p, r);
+    widen_row_words<DT, N>(r, out);
   }
 }
 

@@ -63,8 +63,29 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane >> 4, c = lane & 15;
 
-  // The head's G query rows are read once per workgroup into LDS: every workgroup of a head reads
-  // the same rows, and per-wave reads of them were a hot spot on a few L2 lines.
+  const int wg_begin = split * kBlocksPerWG;
+  const int wg_end = min(n_cand, wg_begin + kBlocksPerWG);
+  const typename E::T* kmin_h = kmin + (int64_t)h * meta_head_stride + (int64_t)cand_offset * D + c * EPL;
+  const typename E::T* kmax_h = kmax + (int64_t)h * meta_head_stride + (int64_t)cand_offset * D + c * EPL;
+  float* bound_h = bounds + (int64_t)h * bound_stride;
+
+  // Every metadata load is issued, raw, before anything waits on one: widened as loaded, the
+  // first row's conversion sat between the two loads and the second waited for the first.
+  lkv::RowWords<MT, EPL> wmax[kIter], wmin[kIter];
+#pragma unroll
+  for (int it = 0; it < kIter; ++it) {
+    const int blk = wg_begin + (it * kBoundWaves + wave) * 4 + r;
+    if (blk < wg_end) {
+      lkv::load_row_words<MT, EPL>(kmax_h + (int64_t)blk * D, wmax[it]);
+      lkv::load_row_words<MT, EPL>(kmin_h + (int64_t)blk * D, wmin[it]);
+    } else {
+#pragma unroll
+      for (int w = 0; w < lkv::RowWords<MT, EPL>::WORDS; ++w) wmax[it].w[w] = wmin[it].w[w] = 0u;
+    }
+  }
+  // The head's G query rows are read once per workgroup into LDS, while the metadata loads above
+  // are in flight: every workgroup of a head reads the same rows, and per-wave reads of them were a
+  // hot spot on a few L2 lines.
   __shared__ float s_q[G * D];
   for (int i = threadIdx.x; i < G * D; i += kBoundThreads) s_q[i] = lkv::load_any(q, (int64_t)h * G * D + i, q_dtype);
   __syncthreads();
@@ -78,35 +99,20 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
       qn[j][e] = x - qp[j][e];
     }
   }
-  const int wg_begin = split * kBlocksPerWG;
-  const int wg_end = min(n_cand, wg_begin + kBlocksPerWG);
-  const typename E::T* kmin_h = kmin + (int64_t)h * meta_head_stride + (int64_t)cand_offset * D + c * EPL;
-  const typename E::T* kmax_h = kmax + (int64_t)h * meta_head_stride + (int64_t)cand_offset * D + c * EPL;
-  float* bound_h = bounds + (int64_t)h * bound_stride;
-
-  float vmax[kIter][EPL], vmin[kIter][EPL];
 #pragma unroll
   for (int it = 0; it < kIter; ++it) {
     const int blk = wg_begin + (it * kBoundWaves + wave) * 4 + r;
-    if (blk < wg_end) {
-      lkv::load_row_segment<MT, EPL>(kmax_h + (int64_t)blk * D, vmax[it]);
-      lkv::load_row_segment<MT, EPL>(kmin_h + (int64_t)blk * D, vmin[it]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) vmax[it][e] = vmin[it][e] = 0.0f;
-    }
-  }
-#pragma unroll
-  for (int it = 0; it < kIter; ++it) {
-    const int blk = wg_begin + (it * kBoundWaves + wave) * 4 + r;
+    float vmax[EPL], vmin[EPL];
+    lkv::widen_row_words<MT, EPL>(wmax[it], vmax);
+    lkv::widen_row_words<MT, EPL>(wmin[it], vmin);
     float best = -INFINITY;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       float a = 0.0f, b = 0.0f;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
-        a = fmaf(qp[j][e], vmax[it][e], a);
-        b = fmaf(qn[j][e], vmin[it][e], b);
+        a = fmaf(qp[j][e], vmax[e], a);
+        b = fmaf(qn[j][e], vmin[e], b);
       }
       float v;
       if (rank_mode == LKV_RANK_MODEL) {
