@@ -105,8 +105,11 @@ def _events(n: int):  # noqa: ANN202
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
-def time_step(step, steps: int, warmup: int, eager: bool) -> tuple[float, float]:  # noqa: ANN001
-    """(ms per step, wall s): `step` captured once in a HIP graph and replayed, or launched eagerly."""
+def time_step(step, steps: int, warmup: int, eager: bool) -> tuple[float, float, dict]:  # noqa: ANN001
+    """(ms per step, wall s, per-step distribution): `step` captured once in a HIP graph and
+    replayed, or launched eagerly. The first two figures time `steps` back-to-back steps between
+    two events; the distribution then times at least 20 (up to 100, about 10 s) further steps
+    each between events of its own, for the median and interquartile range."""
     import torch
 
     step()
@@ -129,8 +132,18 @@ def time_step(step, steps: int, warmup: int, eager: bool) -> tuple[float, float]
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
+    ms = e0.elapsed_time(e1) / steps
+    n = max(20, min(100, int(10_000 / max(ms, 1e-3))))
+    ev = _events(n + 1)
+    ev[0].record()
+    for i in range(n):
+        run()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
+    q1, q2, q3 = statistics.quantiles(per, n=4)
     del graph
-    return e0.elapsed_time(e1) / steps, wall
+    return ms, wall, {"median_ms": q2, "iqr_ms": [q1, q3], "steps": n}
 
 
 def kernel_us(calls: list, reps: int) -> list[float]:
@@ -318,12 +331,13 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             decodes[li]()
         torch.cuda.synchronize()
         assert all(torch.isfinite(o.float()).all() for o in outs), "non-finite output"
-        ms_step, wall = time_step(step, args.steps, args.warmup, args.eager)
+        ms_step, wall, dist = time_step(step, args.steps, args.warmup, args.eager)
         per = [kernel_us([ranks[li], decodes[li]], max(2, min(5, args.steps))) for li in range(L)]
         sel_us = statistics.mean(x[0] for x in per)
         dec_us = statistics.mean(x[1] for x in per)
         log(f"{name}: {ms_step:.3f} ms/step = {ms_step * 1e3 / L:.1f} us/layer (bound+topk {sel_us:.1f} us, decode {dec_us:.1f} us), wall {wall:.2f}s")
-        res[name] = {"k": k, "ms_step": ms_step, "us_layer": ms_step * 1e3 / L, "sel_us": sel_us, "dec_us": dec_us, "host_sel": bool(sels[0].flags), "rem": rems is not None}
+        res[name] = {"k": k, "ms_step": ms_step, "us_layer": ms_step * 1e3 / L, "sel_us": sel_us, "dec_us": dec_us, "host_sel": bool(sels[0].flags), "rem": rems is not None,
+                     "dist": dist}
 
     # ---- probes --------------------------------------------------------------------------------
     probe = {}
@@ -367,6 +381,8 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
         dec_hbm = B_sinkcur + B_q + B_out + (0 if rr["host_sel"] else b_sel)
         legs_out[name] = {
             "k": rr["k"], "us_per_layer": round(rr["us_layer"], 3), "ms_per_step": round(rr["ms_step"], 4),
+            "step_stats": {"us_per_layer_median": round(rr["dist"]["median_ms"] * 1e3 / L, 2),
+                           "us_per_layer_iqr": [round(x * 1e3 / L, 2) for x in rr["dist"]["iqr_ms"]], "steps": rr["dist"]["steps"]},
             "hbm_bytes_per_layer": hb, "pcie_bytes_per_layer": pb,
             "t_roof_us": round(t_roof, 3), "frac": round(t_roof / rr["us_layer"], 4),
             "t_roof_us_at_probe": round(t_probe, 2) if t_probe else None, "frac_at_probe": round(t_probe / rr["us_layer"], 4) if t_probe else None,
@@ -404,6 +420,7 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             "host_memory": "fine-grained" if args.coherent else "coarse-grained",
         },
         "host_syncs_per_layer": 0,
+        "step_stats": dict(m["step_stats"], note="each step replayed between events of its own, after the timed region"),
     }
     # The dominant kernel is lkv_sparse_decode (sparse_decode_kernel + decode_merge_kernel).
     traffic = pmc_traffic() if kind == "host" else {}

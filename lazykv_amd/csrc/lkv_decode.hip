@@ -127,13 +127,18 @@ __device__ __forceinline__ void load_raw(const Src& s, int block, int h, int t0,
   const T* vb = (const T*)s.v + off;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    // Branch-free: a row past `limit` (which may lie past the end of the source) reads the
+    // block's row 0 instead and is zeroed. Loads under a branch, zeros on the other, were merged
+    // by the compiler into stores through a computed address, which kept `raw` in private memory.
     const int row = t0 + r + 4 * i;
-    if (i < nit && row < limit) {  // rows past `limit` may lie past the end of the source
-      load_words(kb + (int64_t)row * D, raw.k[i]);
-      load_words(vb + (int64_t)row * D, raw.v[i]);
-    } else {
+    const bool ok = i < nit && row < limit;
+    const int64_t at = (int64_t)(ok ? row : 0) * D;
+    load_words(kb + at, raw.k[i]);
+    load_words(vb + at, raw.v[i]);
 #pragma unroll
-      for (int w = 0; w < RawModel<D, MT>::W; ++w) raw.k[i][w] = raw.v[i][w] = 0u;
+    for (int w = 0; w < RawModel<D, MT>::W; ++w) {
+      raw.k[i][w] = ok ? raw.k[i][w] : 0u;
+      raw.v[i][w] = ok ? raw.v[i][w] : 0u;
     }
   }
 }
@@ -193,15 +198,18 @@ __device__ __forceinline__ void load_raw(const Src& s, int bs, int block, int h,
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = t0 + r + 4 * i;
-    if (i < nit && row < limit) {
-      load_words(rec + row * D + c * EPL, raw.k[i]);
-      load_words(rec + bs * D + row * D + c * EPL, raw.v[i]);
-      raw.vs[i] = (row & 1) ? wvs[i] >> 16 : wvs[i] & 0xffffu;
-      raw.vz[i] = (row & 1) ? wvz[i] >> 16 : wvz[i] & 0xffffu;
-    } else {
+    // Rows past `limit` are masked before their values are used.
+    raw.vs[i] = (row & 1) ? wvs[i] >> 16 : wvs[i] & 0xffffu;
+    raw.vz[i] = (row & 1) ? wvz[i] >> 16 : wvz[i] & 0xffffu;
+    // Branch-free as for model-dtype rows: a masked row reads row 0 of the record and is zeroed.
+    const bool ok = i < nit && row < limit;
+    const int at = (ok ? row : 0) * D + c * EPL;
+    load_words(rec + at, raw.k[i]);
+    load_words(rec + bs * D + at, raw.v[i]);
 #pragma unroll
-      for (int w = 0; w < RawI8<D>::W; ++w) raw.k[i][w] = raw.v[i][w] = 0u;
-      raw.vs[i] = raw.vz[i] = 0u;
+    for (int w = 0; w < RawI8<D>::W; ++w) {
+      raw.k[i][w] = ok ? raw.k[i][w] : 0u;
+      raw.v[i][w] = ok ? raw.v[i][w] : 0u;
     }
   }
 }
@@ -365,15 +373,19 @@ __device__ __forceinline__ void process_two(const DecodeArgs& a, const Src& s, i
   }
 }
 
-template <int D, int MT, int G>
+// I8: the launch may read int8 records. Without it the int8 code is not compiled in, which keeps
+// the model-dtype kernels' register use down (512-thread workgroups leave no spill registers).
+template <int D, int MT, int G, bool I8>
 __device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, int block_a, int block_b, int h,
                                            int limit, const float (&q)[G][D / 16], int r, int c,
                                            WaveState<D, G>& st) {
-  if (s.dtype == LKV_INT8_RECORD) {
-    process_two<D, MT, G, RawI8<D>>(a, s, block_a, block_b, h, limit, q, r, c, st);
-  } else {
-    process_two<D, MT, G, RawModel<D, MT>>(a, s, block_a, block_b, h, limit, q, r, c, st);
+  if constexpr (I8) {
+    if (s.dtype == LKV_INT8_RECORD) {
+      process_two<D, MT, G, RawI8<D>>(a, s, block_a, block_b, h, limit, q, r, c, st);
+      return;
+    }
   }
+  process_two<D, MT, G, RawModel<D, MT>>(a, s, block_a, block_b, h, limit, q, r, c, st);
 }
 
 // A residency miss: attend `block` of the host source exactly as attend_two does, and copy each
@@ -431,7 +443,7 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
   }
 }
 
-template <int D, int MT, int G, int NT>
+template <int D, int MT, int G, int NT, bool I8>
 __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   constexpr int NW = NT / 64;
   constexpr int EPL = D / 16;
@@ -467,9 +479,9 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     const int last = min(a.n_a, first + a.per_a);
     const int has_sink = a.sink_block >= 0;
     const int n_sel = a.attend_selected ? a.k : 0;
-    if (has_sink && first == 0 && wave == 0) attend_two<D, MT, G>(a, a.sink, a.sink_block, -1, h, a.bs, q, r, c, st);
+    if (has_sink && first == 0 && wave == 0) attend_two<D, MT, G, I8>(a, a.sink, a.sink_block, -1, h, a.bs, q, r, c, st);
     if (a.cur_block >= 0 && last == a.n_a && wave == NW - 1)
-      attend_two<D, MT, G>(a, a.cur, a.cur_block, -1, h, a.fill, q, r, c, st);
+      attend_two<D, MT, G, I8>(a, a.cur, a.cur_block, -1, h, a.fill, q, r, c, st);
     // Selected items of this run: idx positions [js, je), two per wave per round.
     const int js = max(first, has_sink) - has_sink;
     const int je = min(last, has_sink + n_sel) - has_sink;
@@ -480,18 +492,21 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
         const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
         if (l >= 0 && (l & kLocMiss)) {
-          if (a.sel.dtype == LKV_INT8_RECORD) {
-            attend_fill_i8<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
-          } else {
-            attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
+          bool filled = false;
+          if constexpr (I8) {
+            if (a.sel.dtype == LKV_INT8_RECORD) {
+              attend_fill_i8<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
+              filled = true;
+            }
           }
+          if (!filled) attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
         } else if (l >= 0) {
-          attend_two<D, MT, G>(a, a.slots, l, -1, h, a.bs, q, r, c, st);
+          attend_two<D, MT, G, I8>(a, a.slots, l, -1, h, a.bs, q, r, c, st);
         }
         continue;
       }
       const int b1 = (kPairs<G> == 2 && j + NW < je) ? idx_h[j + NW] : -1;
-      attend_two<D, MT, G>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
+      attend_two<D, MT, G, I8>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
     }
   } else {
     // Segment B: remainder blocks of this run that idx does not name.
@@ -519,7 +534,7 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
         if (!((s_excl[(b - lo) >> 5] >> ((b - lo) & 31)) & 1u)) pick[have++] = b;
         b += NW;
       }
-      if (have) attend_two<D, MT, G>(a, a.rem, pick[0], pick[1], h, a.bs, q, r, c, st);
+      if (have) attend_two<D, MT, G, I8>(a, a.rem, pick[0], pick[1], h, a.bs, q, r, c, st);
     }
   }
 
@@ -715,15 +730,24 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
 template <int D, int MT, int G>
 int launch(hipStream_t stream, DecodeArgs& a) {
   const int S = a.splits_a + a.splits_b;
+  const bool i8 = a.sel.dtype == LKV_INT8_RECORD || a.rem.dtype == LKV_INT8_RECORD || a.sink.dtype == LKV_INT8_RECORD ||
+                  a.cur.dtype == LKV_INT8_RECORD;
   bool launched = false;
   if constexpr (G <= 4) {
     if (a.nt == kThreadsHbm) {
-      hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
-      launched = true;
+      // The int8-capable 512-thread kernel spills at D = 128, G = 4; such a launch takes the
+      // 256-thread kernel over the same plan (its waves stride the same runs of items).
+      if (!i8) {
+        hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
+        launched = true;
+      } else if constexpr (!(D == 128 && G == 4)) {
+        hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, true>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
+        launched = true;
+      }
     }
   }
   if (!launched) {
-    hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreads>), dim3(S * a.n_kv), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreads, true>), dim3(S * a.n_kv), dim3(kThreads), 0, stream, a);
   }
   LKV_CHECK_LAUNCH("sparse_decode");
   hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(512), 0, stream, a.part_ml, a.part_o, S,
