@@ -43,6 +43,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+DENSE_LAYERS = 2  # the reference's default dense layers, for the int8_64k variant that keeps them
 METRIC = "decode-step µs/layer & achieved HBM GB/s (% roofline) at 128K ctx, 6.25% budget"
 HBM_PEAK_GBPS = 8000.0
 PCIE_PEAK_GBPS = 64.0  # PCIe Gen5 x16, one direction
@@ -282,6 +283,8 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             st["host"] = host
         if want_hbm_leg or kind == "exact":
             st["pool"] = pool
+        if kind == "int8" and li < DENSE_LAYERS:  # the 2-dense variant keeps these layers' full KV in HBM
+            st["dense"] = (w.keys, w.values)
         del w, pool, src
         layers.append(st)
         if li % 8 == 7:
@@ -300,6 +303,9 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
         legs.append(("hbm", ks[0], [kernels.pool_source(st["pool"]) for st in layers], None))
     elif kind == "int8":
         legs.append((f"int8_{args.tier_where}", ks[0], [kernels.record_source(st["records"], dtype) for st in layers], None))
+        # The reference's default keeps the first two layers dense (lazykv/selection.py:35): those
+        # layers attend all their tokens from HBM, the other 14 select from the int8 tier.
+        legs.append((f"int8_{args.tier_where}_{DENSE_LAYERS}dense", ks[0], [kernels.record_source(st["records"], dtype) for st in layers], None))
     else:
         for k in ks:
             legs.append((f"exact_k{k}", k, [kernels.pool_source(st["pool"]) for st in layers], [kernels.record_source(st["records"], dtype) for st in layers]))
@@ -309,9 +315,16 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
     ws_sel, ws_dec = kernels.Workspace(dev), kernels.Workspace(dev)
     res = {}
     for name, k, sels, rems in legs:
+        n_dense = DENSE_LAYERS if name.endswith("dense") else 0
         idx = torch.empty((H, k), dtype=torch.int32, device=dev)
         ranks, decodes = [], []
         for li, st in enumerate(layers):
+            if li < n_dense:  # dense decode: every block of the layer's KV, from HBM
+                dsrc = kernels.dense_source(st["dense"][0], st["dense"][1], BS)
+                ranks.append(None)
+                decodes.append(kernels.PreparedDecode(st["q"], n_kv=H, block_size=BS, scale=scale, sel=None, idx=None, sink=None, sink_block=-1, cur=None, cur_block=-1,
+                                                      fill=0, out=outs[li], lse=lses[li], rem=dsrc, rem_range=(0, N), attend_selected=False, ws=ws_dec))
+                continue
             ranks.append(kernels.PreparedBoundTopk(st["q"], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx, ws=ws_sel))
             ss = kernels.pool_source(st["slots"])
             extra = dict(rem=rems[li], rem_range=(1, n_sealed)) if rems is not None else {}
@@ -320,24 +333,29 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
 
         def step(ranks=ranks, decodes=decodes) -> None:  # noqa: ANN001
             for rk, dc in zip(ranks, decodes):
-                rk()
+                if rk is not None:
+                    rk()
                 dc()
 
-        # Every layer's needle is selected for every KV head; outputs are finite.
+        # Every selecting layer's needle is selected for every KV head; outputs are finite.
         for li in range(L):
-            ranks[li]()
-            got = idx.cpu()
-            assert (got == layers[li]["needle"]).any(dim=1).all(), f"layer {li}: needle block {layers[li]['needle']} not selected"
+            if ranks[li] is not None:
+                ranks[li]()
+                got = idx.cpu()
+                assert (got == layers[li]["needle"]).any(dim=1).all(), f"layer {li}: needle block {layers[li]['needle']} not selected"
             decodes[li]()
         torch.cuda.synchronize()
         assert all(torch.isfinite(o.float()).all() for o in outs), "non-finite output"
         ms_step, wall, dist = time_step(step, args.steps, args.warmup, args.eager)
-        per = [kernel_us([ranks[li], decodes[li]], max(2, min(5, args.steps))) for li in range(L)]
+        reps = max(2, min(5, args.steps))
+        per = [kernel_us([ranks[li], decodes[li]], reps) for li in range(n_dense, L)]
         sel_us = statistics.mean(x[0] for x in per)
         dec_us = statistics.mean(x[1] for x in per)
-        log(f"{name}: {ms_step:.3f} ms/step = {ms_step * 1e3 / L:.1f} us/layer (bound+topk {sel_us:.1f} us, decode {dec_us:.1f} us), wall {wall:.2f}s")
+        dense_us = statistics.mean(kernel_us([decodes[li]], reps)[0] for li in range(n_dense)) if n_dense else None
+        extra = f", dense decode {dense_us:.1f} us on {n_dense} layers" if n_dense else ""
+        log(f"{name}: {ms_step:.3f} ms/step = {ms_step * 1e3 / L:.1f} us/layer (bound+topk {sel_us:.1f} us, decode {dec_us:.1f} us{extra}), wall {wall:.2f}s")
         res[name] = {"k": k, "ms_step": ms_step, "us_layer": ms_step * 1e3 / L, "sel_us": sel_us, "dec_us": dec_us, "host_sel": bool(sels[0].flags), "rem": rems is not None,
-                     "dist": dist}
+                     "dist": dist, "n_dense": n_dense, "dense_us": dense_us}
 
     # ---- probes --------------------------------------------------------------------------------
     probe = {}
@@ -363,12 +381,18 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
     B_sinkcur = 2 * H * 2 * BS * d * es
 
     def leg_bytes(rr: dict) -> tuple[int, int, int, int]:
-        """(selected bytes, remainder bytes, HBM bytes per layer, PCIe bytes per layer)."""
+        """(selected bytes, remainder bytes, HBM bytes per layer, PCIe bytes per layer); with dense
+        layers, the step's bytes averaged over its layers."""
         k = rr["k"]
         b_sel = H * k * P if kind == "int8" else 2 * H * k * BS * d * es
         b_rem = H * (n_cand - k) * P if rr["rem"] else 0
         hbm = B_meta + 2 * B_q + B_out + B_sinkcur + (0 if rr["host_sel"] else b_sel)
         pcie = (b_sel if rr["host_sel"] else 0) + b_rem
+        nd = rr["n_dense"]
+        if nd:
+            dense = 2 * H * N * BS * d * es + B_q + B_out  # all K and V of the layer
+            hbm = ((L - nd) * hbm + nd * dense) // L
+            pcie = (L - nd) * pcie // L
         return b_sel, b_rem, hbm, pcie
 
     legs_out = {}
@@ -391,6 +415,10 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             "sparse_decode_pcie_gbps": round(dec_pcie / (rr["dec_us"] * 1e-6) / 1e9, 2) if dec_pcie else None,
             "sparse_decode_hbm_gbps": round(dec_hbm / (rr["dec_us"] * 1e-6) / 1e9, 1),
         }
+        if rr["n_dense"]:
+            dense_bytes = 2 * H * N * BS * d * es
+            legs_out[name].update(dense_layers=rr["n_dense"], dense_decode_us=round(rr["dense_us"], 2),
+                                  dense_decode_hbm_gbps=round(dense_bytes / (rr["dense_us"] * 1e-6) / 1e9, 1))
 
     main_leg = next(iter(res))
     m = legs_out[main_leg]

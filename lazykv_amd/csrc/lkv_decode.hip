@@ -708,6 +708,15 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
     p.per_a = (p.n_a + per_head - 1) / per_head;
     if (p.per_a < kThreadsHbm / 64) p.per_a = kThreadsHbm / 64;
     p.splits_a = p.n_a > 0 ? (p.n_a + p.per_a - 1) / p.per_a : 0;
+    // The remainder too: about one workgroup per CU, each wave streaming its share of the run.
+    // Measured on a dense decode (every block a remainder block): 128K tokens, bf16 d128, 130 us
+    // at 32 runs per head against 169 us at 256 runs (fewer runs than CUs leave CUs idle).
+    if (n_b > 0) {
+      p.per_b = (n_b + per_head - 1) / per_head;
+      if (p.per_b < kThreadsHbm / 64) p.per_b = kThreadsHbm / 64;
+      if (p.per_b > 2048) p.per_b = 2048;  // the exclusion bitmap holds 2048 blocks
+      p.splits_b = (n_b + p.per_b - 1) / p.per_b;
+    }
   }
   if (hint.sel_host && n_sel > 0) {
     const int s = host_splits(hint.sel_pair, d->n_kv, lkv_host_read_inflight());
