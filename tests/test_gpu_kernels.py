@@ -292,6 +292,52 @@ def test_sparse_decode_matches_the_oracle(where: str, h: int, g: int, n: int, d:
     assert torch.equal(out_bf, out.to(torch.bfloat16)) and torch.equal(lse_bf, lse)
 
 
+@pytest.mark.parametrize("where", ["hbm", "host"])
+@pytest.mark.parametrize("src_kind", ["f16", "bf16", "f32", "int8/f16", "int8/bf16"])
+@pytest.mark.parametrize(("bs", "d", "fill"), [(4, 64, 1), (8, 128, 8), (20, 64, 3), (20, 128, 17), (32, 64, 32), (64, 128, 50)])
+def test_sparse_decode_block_sizes_and_dtypes(where: str, src_kind: str, bs: int, d: int, fill: int) -> None:
+    """Every block size the kernels take (multiples of 4 up to 64, including chunks shorter than
+    16 rows and a 4-row tail chunk at bs 20), partial and full current blocks, each model dtype and
+    int8 records (read in place, dequantised in the load), from HBM and from host memory."""
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+    from lazykv_amd.quant import packed_pair_bytes
+
+    h, g, n, k = 4, 4, 60, 12
+    int8 = src_kind.startswith("int8")
+    dt = src_kind.split("/")[-1]
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dt]
+    w, pool = _pool_case(bs * 1000 + d + len(src_kind), h, g, n, bs, d, torch.float16 if dt == "f32" else tdt)
+    pool = pool.to(tdt)
+    gen = torch.Generator().manual_seed(bs + d)
+    chosen = torch.stack([torch.randperm(n - 2, generator=gen)[:k] + 1 for _ in range(h)]).to(torch.int32)
+    exact = _f64(pool)
+    if int8:
+        recs = R.pack(_bits(pool), dt)  # [n, h, P]
+        store = pinned_empty((n, h, packed_pair_bytes(bs, d)), torch.uint8) if where == "host" else torch.empty((n, h, packed_pair_bytes(bs, d)), dtype=torch.uint8).cuda()
+        store.copy_(torch.from_numpy(recs))
+        sel = kernels.record_source(store, tdt)
+        deq = R.to_f32(R.unpack(recs.reshape(n * h, -1), bs, d, dt), dt).reshape(n, h, 2, bs, d).astype(np.float64)
+    else:
+        store = pinned_empty(tuple(pool.shape), tdt) if where == "host" else torch.empty(tuple(pool.shape), dtype=tdt).cuda()
+        store.copy_(pool)
+        sel = kernels.pool_source(store)
+        deq = exact
+    slots = pool[[0, n - 1]].contiguous().cuda()  # sink and current in the model dtype
+    ss = kernels.pool_source(slots)
+    out, lse = kernels.sparse_decode(w.query.to(tdt).cuda(), n_kv=h, block_size=bs, scale=d**-0.5, sel=sel, idx=chosen.cuda(), sink=ss, sink_block=0, cur=ss, cur_block=1,
+                                     fill=fill, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+
+    def bkv(j, b):
+        src = exact if b in (0, n - 1) else deq
+        return src[b, j, 0], src[b, j, 1]
+
+    want_o, want_l = _oracle_decode(w.query.to(tdt), exact, chosen.numpy(), 0, n - 1, fill, d**-0.5, bs, bkv)
+    assert np.abs(out.cpu().numpy() - want_o).max() < TOL
+    assert np.abs(lse.cpu().numpy() - want_l).max() < TOL
+
+
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 def test_sparse_decode_reads_int8_records_in_place(dt: str) -> None:
     from lazykv_amd import kernels
