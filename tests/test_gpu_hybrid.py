@@ -37,6 +37,9 @@ def _layer(seed: int, h: int, g: int, n: int, bs: int, d: int, dt: torch.dtype):
         (2, 8, 150, 32, 128, 40, torch.bfloat16, 19, None),
         (8, 4, 300, 16, 128, 32, torch.bfloat16, 16, "int8"),
         (4, 4, 200, 16, 64, 24, torch.float16, 5, "int8"),
+        (4, 4, 120, 20, 64, 16, torch.float16, 7, "int8"),  # a 4-row tail chunk per pair
+        (2, 8, 100, 64, 128, 20, torch.bfloat16, 50, "int8"),
+        (4, 2, 160, 8, 128, 30, torch.bfloat16, 8, None),
     ],
 )
 def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, fill: int, quant: str | None) -> None:
