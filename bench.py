@@ -181,6 +181,24 @@ def probe_gbps(addr: int, nbytes: int, blocks: int, reps: int = 5) -> float:
     return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
 
+def dma_h2d_gbps(host, reps: int = 3) -> float:  # noqa: ANN001
+    """The copy engines' host-to-device rate over the same pinned pool (a plain hipMemcpyAsync):
+    the link's practical ceiling, to set the kernels' reads beside."""
+    import torch
+
+    src = host.reshape(-1).view(torch.uint8)[: 512 << 20]
+    dst = torch.empty_like(src, device="cuda")
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src, non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize()
+    return src.numel() * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
 def pmc_traffic() -> dict:
     """Calibrated HBM/fabric bytes per launch, per "<leg>/<kernel>", from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary of the default workload (a counter run cannot time itself)."""
@@ -369,6 +387,7 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             break
     if host_buf is not None:
         probe["pcie_read_gbps"] = probe_gbps(device_address(host_buf), host_buf.numel() * host_buf.element_size() // 16 * 16, 2048)
+        probe["dma_h2d_gbps"] = dma_h2d_gbps(host_buf)
     big = torch.empty(4 << 30, dtype=torch.uint8, device=dev)
     probe["hbm_read_gbps"] = probe_gbps(big.data_ptr(), big.numel(), 4096)
     del big
@@ -457,6 +476,9 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
         out["roofline"] = {"bound": "pcie", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, host reads over PCIe", "achieved": gbps,
                            "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get("zerocopy/sparse_decode_kernel"),
                            "algorithmic_bytes": m["sparse_decode_pcie_bytes"], "kernel_us": m["sparse_decode_us"]}
+        if probe.get("dma_h2d_gbps"):
+            out["roofline"]["link_ceiling_gbps"] = round(probe["dma_h2d_gbps"], 2)  # the copy engines over the same pool
+            out["roofline"]["frac_of_link_ceiling"] = round(gbps / probe["dma_h2d_gbps"], 4)
         if traffic:
             out["roofline"]["traffic_note"] = ("calibrated FETCH_SIZE + WRITE_SIZE bytes per launch, host (PCIe) and HBM fetches together; algorithmic total incl. HBM part "
                                                f"{m['sparse_decode_pcie_bytes'] + m['sparse_decode_hbm_bytes']}; source {TRAFFIC_FILE.relative_to(ROOT)}")
