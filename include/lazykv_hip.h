@@ -142,7 +142,9 @@ int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void*
  * residency with the zero-copy read. Per KV head, `slots` holds k slots of pairs in HBM; the
  * tables block_slot[h * block_slot_stride + b] (slot or -1) and slot_block[h * slot_block_stride +
  * s] (block or -1) say which blocks they hold; the caller allocates them on the device and fills
- * them with -1 once. Each call first updates the tables for the selection idx: with as many slots
+ * them with -1 once. A block counts as resident only where both tables agree, so tables left
+ * inconsistent (or filled with zeros) cost misses, not wrong reads. Each call first updates the
+ * tables for the selection idx: with as many slots
  * as selected blocks, the slots the selection does not hit are exactly the victims, taken in
  * ascending slot order by the missed blocks in ascending block order. It then attends as
  * lkv_sparse_decode does over `host` (mapped host memory: model-dtype pairs, or int8 records as in

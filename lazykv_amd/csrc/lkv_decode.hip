@@ -12,11 +12,12 @@
 //
 // Work split. Per KV head h the items are [sink, idx[h][0..k), current] (segment A) and the
 // remainder blocks [rem_first, rem_last) not in idx (segment B). blockIdx.x % n_kv is the head,
-// so one head's workgroups share an XCD and its L2. Each workgroup (4 waves) takes a run of
-// items; each wave handles one (block, head) pair at a time with all G query heads of the group,
-// so every KV byte is read once. Lane l holds row (l >> 4) + 4i of the block, channels
-// (l & 15) * D/16 ..: one 16-byte load per lane covers 4 rows. Scores are 16-lane DPP sums; the
-// online softmax runs in base 2 with the scale folded into q.
+// so one head's workgroups share an XCD and its L2. Each workgroup (4 waves when the launch reads
+// host memory, 8 when everything is in HBM) takes a run of items; each wave handles one
+// (block, head) pair at a time with all G query heads of the group, so every KV byte is read
+// once. Lane l holds row (l >> 4) + 4i of the block, channels (l & 15) * D/16 ..: at d 128 in
+// bf16, one 16-byte load per lane covers 4 rows. Scores are 16-lane DPP sums; the online softmax
+// runs in base 2 with the scale folded into q.
 //
 // Merge. Waves combine in LDS, workgroups write (m, l, o) partials to the workspace, and a second
 // launch folds each query head's partials into out and lse. (A last-arriver merge inside one
@@ -833,8 +834,14 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
     blk[u] = (u < per && i < k) ? idx_h[i] : -1;
     const bool valid = blk[u] >= 0 && (int64_t)blk[u] < n_blocks;
     cur[u] = valid ? bslot_h[blk[u]] : -2;  // -2: not a block of the pool; -1: not resident
-    if (cur[u] >= n_slots) cur[u] = -1;      // a stale table entry cannot name a slot
+    if (valid && (cur[u] < 0 || cur[u] >= n_slots)) cur[u] = -1;  // an entry that names no slot: not resident
   }
+  // A hit needs both tables to agree (block_slot[b] = s and slot_block[s] = b): tables a caller
+  // left inconsistent (or filled with zeros instead of -1) can then cost misses, never a read of
+  // a slot that holds another block.
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u)
+    if (cur[u] >= 0 && sblock_h[cur[u]] != blk[u]) cur[u] = -1;
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < kResPer; ++u)
@@ -872,7 +879,9 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
     } else {
       const int v = victims[mpos++];
       const int32_t old = sblock_h[v];
-      if (old >= 0 && (int64_t)old < n_blocks) bslot_h[old] = -1;  // `old` is unselected: no other item writes it
+      // Only an entry that points back at v is cleared: then `old` was resident in v, and as v is
+      // unhit, `old` is unselected, so no other item writes its entry.
+      if (old >= 0 && (int64_t)old < n_blocks && bslot_h[old] == v) bslot_h[old] = -1;
       sblock_h[v] = blk[u];
       bslot_h[blk[u]] = v;
       loc_h[i] = kLocMiss | v;

@@ -83,6 +83,51 @@ def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, 
     assert hits > 0  # the drift keeps part of each selection resident
 
 
+@pytest.mark.parametrize("tables", ["zeros", "garbage"])
+def test_hybrid_decode_survives_tables_that_disagree(tables: str) -> None:
+    """Tables filled with zeros instead of -1, or with out-of-range and contradictory entries: a
+    hit needs block_slot and slot_block to agree, so every step still equals the zero-copy
+    decode, and after it the selected blocks are resident with consistent tables. (A pair of
+    entries that agree is a residency claim, which no table check can tell from a true one.)"""
+    from lazykv_amd import kernels
+
+    h, g, n, bs, d, k = 4, 4, 120, 16, 64, 16
+    w, pool, host, kmin, kmax = _layer(5, h, g, n, bs, d, torch.float16)
+    res = kernels.Residency.allocate(k, h, n, bs, d, torch.float16, torch.device("cuda"))
+    gen = torch.Generator().manual_seed(9)
+    if tables == "zeros":
+        res.block_slot.zero_()
+        res.slot_block.zero_()
+    else:  # out-of-range and contradictory entries; no pair that agrees (that would be a residency claim)
+        bsl = torch.randint(-9, k + 9, (h, n), generator=gen, dtype=torch.int32)
+        sbl = torch.randint(-9, n + 9, (h, k), generator=gen, dtype=torch.int32)
+        for j in range(h):
+            for s_ in range(k):
+                b = int(sbl[j, s_])
+                if 0 <= b < n and int(bsl[j, b]) == s_:
+                    sbl[j, s_] = -5
+        res.block_slot.copy_(bsl.cuda())
+        res.slot_block.copy_(sbl.cuda())
+    res.slots.normal_()  # slot contents that no table entry may be trusted to describe
+    ss = kernels.pool_source(pool[[0, n - 1]].contiguous())
+    hsrc = kernels.pool_source(host)
+    q0 = w.query.float()
+    for step in range(4):
+        q = (q0 + 0.3 * torch.randn(q0.shape, generator=gen)).to(torch.float16).cuda()
+        idx = kernels.bound_topk(q, kmin, kmax, k, cand_offset=1, n_cand=n - 2)
+        common = dict(n_kv=h, block_size=bs, scale=d**-0.5, idx=idx, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=5, out_dtype=torch.float32)
+        out_z, lse_z = kernels.sparse_decode(q, sel=hsrc, **common)
+        out_h, lse_h = kernels.hybrid_decode(q, host=hsrc, res=res, **common)
+        torch.cuda.synchronize()
+        assert torch.equal(out_h, out_z) and torch.equal(lse_h, lse_z), step
+        bsl, sbl = res.block_slot.cpu(), res.slot_block.cpu()
+        for j in range(h):
+            for b in idx[j].cpu().tolist():
+                s_ = int(bsl[j, b])
+                assert 0 <= s_ < k and int(sbl[j, s_]) == b, (step, j, b)
+                assert torch.equal(res.slots[s_, j], pool[b, j].cuda())
+
+
 def test_hybrid_decode_refuses_what_it_cannot_hold() -> None:
     from lazykv_amd import kernels
 
