@@ -12,8 +12,8 @@
 // its channels of the G query heads in registers. The row sum is a 4-step DPP reduction; the max
 // over the group is taken in registers. The float32 bounds go to a scratch row per head.
 //
-// select_kernel: one 512-thread workgroup per KV head; each thread holds a contiguous run of up to
-// 24 candidates as order-preserving integer keys in registers. The K-th largest is found by
+// select_kernel: one 1024-thread workgroup per KV head; each thread holds a contiguous run of up to
+// 12 candidates as order-preserving integer keys in registers. The K-th largest is found by
 // range-adaptive radix select: each pass
 // histograms the keys of the current range into at most 2048 bins scaled to that range (so the
 // first pass spreads the clustered bounds instead of piling them into a few exponent bins) and
@@ -37,10 +37,11 @@ constexpr int kBoundThreads = LKV_BOUND_THREADS;
 constexpr int kBoundWaves = kBoundThreads / 64;
 constexpr int kIter = LKV_BOUND_ITER;                     // 4-block rows per wave
 constexpr int kBlocksPerWG = kBoundWaves * 4 * kIter;     // candidate blocks per workgroup
-constexpr int kSelThreads = 512;
+constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kBins = 2048;
-constexpr int kPerThread = 24;                            // candidate keys held per thread
+constexpr int kPerThread = 12;                            // candidate keys held per thread
+static_assert(kPerThread <= 32, "a thread's candidate slots are tracked in 32-bit masks");
 constexpr int kMaxCand = kSelThreads * kPerThread;        // 12288 candidates per KV head
 constexpr int kMaxSortedK = 2048;
 
