@@ -259,6 +259,17 @@ __device__ __forceinline__ float row16_min(float x) {
   return x;
 }
 
+// Sum over the LPR lanes of a row (16 or 8); every lane of the row receives the total.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x) {
+  static_assert(LPR == 16 || LPR == 8, "rows are 16 or 8 lanes wide");
+  x += dpp<kDppQuadSwap1>(x);
+  x += dpp<kDppQuadSwap2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  if constexpr (LPR == 16) x += dpp<kDppMirror>(x);
+  return x;
+}
+
 // Combine the four 16-lane row groups of a wave (lanes l, l^16, l^32, l^48).
 __device__ __forceinline__ float xor_lane(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
@@ -278,15 +289,18 @@ __device__ __forceinline__ float groups4_min(float x) {
   return x;
 }
 
-// Release this thread's prior global writes at device scope, then count one arrival on
-// `counter`; returns the previous count. Acquire on the returning side is `acquire_device()`.
-__device__ __forceinline__ void release_device() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-__device__ __forceinline__ void acquire_device() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
-__device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
-  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+// Combine the RG row groups of a wave (rows of 64 / RG lanes: lanes l, l ^ (64/RG), ...).
+template <int RG>
+__device__ __forceinline__ float groups_sum(float x) {
+#pragma unroll
+  for (int m = 64 / RG; m < 64; m <<= 1) x += xor_lane(x, m);
+  return x;
 }
-__device__ __forceinline__ void reset_counter(uint32_t* counter) {
-  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <int RG>
+__device__ __forceinline__ float groups_max(float x) {
+#pragma unroll
+  for (int m = 64 / RG; m < 64; m <<= 1) x = fmaxf(x, xor_lane(x, m));
+  return x;
 }
 
 }  // namespace lkv

@@ -15,9 +15,9 @@
 // so one head's workgroups share an XCD and its L2. Each workgroup (4 waves when the launch reads
 // host memory, 8 when everything is in HBM) takes a run of items; each wave handles one
 // (block, head) pair at a time with all G query heads of the group, so every KV byte is read
-// once. Lane l holds row (l >> 4) + 4i of the block, channels (l & 15) * D/16 ..: at d 128 in
-// bf16, one 16-byte load per lane covers 4 rows. Scores are 16-lane DPP sums; the online softmax
-// runs in base 2 with the scale folded into q.
+// once. A row's channels are spread over 16 lanes at d 128 and 8 lanes at d 64, 8 channels each
+// (Lanes<D>), so a wave-wide load of 16-byte lane segments covers 4 or 8 rows. Scores are DPP
+// sums over a row's lanes; the online softmax runs in base 2 with the scale folded into q.
 //
 // Merge. Waves combine in LDS, workgroups write (m, l, o) partials to the workspace, and a second
 // launch folds each query head's partials into out and lse. (A last-arriver merge inside one
@@ -35,6 +35,18 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kThreadsHbm = 512;
 constexpr int kMaxSplits = 512;  // partials per KV head
+
+// Lane layout of a KV row. LPR lanes hold one row's D channels, EPL each; a wave-wide load covers
+// RG = 64 / LPR rows, so a 16-row chunk takes NI = 16 / RG loads. Both head sizes give each lane 8
+// channels (16 bytes of a 2-byte type): d 128 as 16 lanes x 4 rows, d 64 as 8 lanes x 8 rows. The
+// narrower rows halve the per-row reduction steps and row iterations of a d 64 chunk.
+template <int D>
+struct Lanes {
+  static constexpr int LPR = D == 128 ? 16 : 8;
+  static constexpr int EPL = D / LPR;
+  static constexpr int RG = 64 / LPR;
+  static constexpr int NI = 16 / RG;
+};
 
 struct Src {
   const void* k;
@@ -76,26 +88,28 @@ constexpr int32_t kLocMiss = 0x40000000;
 
 // Raw register image of one chunk (up to 16 tokens) of a pair, exactly as loaded; it is widened
 // to float only when consumed, so a wave can keep two pairs' loads in flight in few registers.
-// Rows r + 4i (i < 4) of the chunk, this lane's D/16 channels.
+// Rows r + RG*i (i < NI) of the chunk, this lane's EPL channels.
 template <int D, int MT>
 struct RawModel {
-  static constexpr int EPL = D / 16;
+  static constexpr int EPL = Lanes<D>::EPL;
+  static constexpr int NI = Lanes<D>::NI;
   static constexpr int W = EPL * (int)sizeof(typename lkv::Elem<MT>::T) / 4;  // words per row segment
-  uint32_t k[4][W];
-  uint32_t v[4][W];
+  uint32_t k[NI][W];
+  uint32_t v[NI][W];
 };
 
 // int8 record of lazykv/quant.py:46-56: kq[bs][D] | vq[bs][D] | ks[D] | kz[D] | vs[bs] | vz[bs].
 template <int D>
 struct RawI8 {
-  static constexpr int EPL = D / 16;
+  static constexpr int EPL = Lanes<D>::EPL;
+  static constexpr int NI = Lanes<D>::NI;
   static constexpr int W = EPL / 4;  // int8 words per row segment
-  uint32_t k[4][W];
-  uint32_t v[4][W];
+  uint32_t k[NI][W];
+  uint32_t v[NI][W];
   uint32_t ks[EPL / 2];  // float16 pairs of this lane's channels
   uint32_t kz[EPL / 2];
-  uint32_t vs[4];  // float16 in the low half
-  uint32_t vz[4];
+  uint32_t vs[NI];  // float16 in the low half
+  uint32_t vz[NI];
 };
 
 template <int W>
@@ -122,16 +136,17 @@ template <int D, int MT>
 __device__ __forceinline__ void load_raw(const Src& s, int block, int h, int t0, int nit, int limit, int r, int c,
                                          RawModel<D, MT>& raw) {
   using T = typename lkv::Elem<MT>::T;
-  constexpr int EPL = D / 16;
+  using L = Lanes<D>;
+  constexpr int EPL = L::EPL;
   const int64_t off = (int64_t)block * s.bstride + (int64_t)h * s.hstride + c * EPL;
   const T* kb = (const T*)s.k + off;
   const T* vb = (const T*)s.v + off;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < L::NI; ++i) {
     // Branch-free: a row past `limit` (which may lie past the end of the source) reads the
     // block's row 0 instead and is zeroed. Loads under a branch, zeros on the other, were merged
     // by the compiler into stores through a computed address, which kept `raw` in private memory.
-    const int row = t0 + r + 4 * i;
+    const int row = t0 + r + L::RG * i;
     const bool ok = i < nit && row < limit;
     const int64_t at = (int64_t)(ok ? row : 0) * D;
     load_words(kb + at, raw.k[i]);
@@ -159,17 +174,18 @@ __device__ __forceinline__ void store_words(void* p, const uint32_t (&w)[W]) {
 // The inverse of load_raw for a model-dtype chunk: the rows this lane loaded, written to `block`
 // of `s` (a slot pool being filled while the pair is attended).
 template <int D, int MT>
-__device__ __forceinline__ void store_raw(const Src& s, int block, int h, int t0, int nit, int r, int c,
+__device__ __forceinline__ void store_raw(const Src& s, int block, int h, int t0, int nit, int bs, int r, int c,
                                           const RawModel<D, MT>& raw) {
   using T = typename lkv::Elem<MT>::T;
-  constexpr int EPL = D / 16;
+  using L = Lanes<D>;
+  constexpr int EPL = L::EPL;
   const int64_t off = (int64_t)block * s.bstride + (int64_t)h * s.hstride + c * EPL;
   T* kb = (T*)s.k + off;
   T* vb = (T*)s.v + off;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (i < nit) {
-      const int row = t0 + r + 4 * i;
+  for (int i = 0; i < L::NI; ++i) {
+    const int row = t0 + r + L::RG * i;
+    if (i < nit && row < bs) {  // a short last chunk leaves rows of its last load past the block
       store_words(kb + (int64_t)row * D, raw.k[i]);
       store_words(vb + (int64_t)row * D, raw.v[i]);
     }
@@ -179,26 +195,31 @@ __device__ __forceinline__ void store_raw(const Src& s, int block, int h, int t0
 template <int D>
 __device__ __forceinline__ void load_raw(const Src& s, int bs, int block, int h, int t0, int nit, int limit, int r, int c,
                                          RawI8<D>& raw) {
-  constexpr int EPL = D / 16;
+  using L = Lanes<D>;
+  constexpr int EPL = L::EPL;
   const uint8_t* rec = (const uint8_t*)s.k + (int64_t)block * s.bstride + (int64_t)h * s.hstride;
   const uint16_t* scales = (const uint16_t*)(rec + 2 * bs * D);
   load_words(scales + c * EPL, raw.ks);
   load_words(scales + D + c * EPL, raw.kz);
-  // The chunk's value scales and zeros in one 64-byte read: lane c < 8 of each row group loads
-  // the float16 pair vs[t0 + 2c, +1], lane c >= 8 the pair vz[t0 + 2(c - 8), +1] (pairs past the
-  // record's bs rows are not read). Each row's pair is then taken from the lane holding it.
-  const int m = c & 7;
-  const uint32_t sz = t0 + 2 * m + 2 <= bs ? *(const uint32_t*)(scales + 2 * D + (c >> 3) * bs + t0 + 2 * m) : 0u;
-  uint32_t wvs[4], wvz[4];
+  // The chunk's value scales and zeros in one 64-byte read per row group, as float16 pairs: with
+  // 16-lane rows, lane c < 8 loads the pair vs[t0 + 2c, +1] and lane c >= 8 the pair vz[t0 + 2(c - 8), +1];
+  // with 8-lane rows, lane c loads both vs[t0 + 2c, +1] and vz[t0 + 2c, +1]. Pairs past the record's bs
+  // rows are not read. Each row's pair is then taken from the lane of its group that holds it.
+  const int m = L::LPR == 16 ? (c & 7) : c;
+  const bool in_rec = t0 + 2 * m + 2 <= bs;
+  const uint32_t sv = in_rec ? *(const uint32_t*)(scales + 2 * D + (L::LPR == 16 ? (c >> 3) * bs : 0) + t0 + 2 * m) : 0u;
+  const uint32_t svz = (L::LPR == 8 && in_rec) ? *(const uint32_t*)(scales + 2 * D + bs + t0 + 2 * m) : sv;
+  const int base = r * L::LPR;  // first lane of this row group
+  uint32_t wvs[L::NI], wvz[L::NI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {  // every lane takes part in the shuffles
-    const int local = r + 4 * i;
-    wvs[i] = (uint32_t)__shfl((int)sz, (r << 4) + (local >> 1));
-    wvz[i] = (uint32_t)__shfl((int)sz, (r << 4) + 8 + (local >> 1));
+  for (int i = 0; i < L::NI; ++i) {  // every lane takes part in the shuffles
+    const int local = r + L::RG * i;
+    wvs[i] = (uint32_t)__shfl((int)sv, base + (local >> 1));
+    wvz[i] = (uint32_t)__shfl((int)svz, base + (L::LPR == 16 ? 8 : 0) + (local >> 1));
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = t0 + r + 4 * i;
+  for (int i = 0; i < L::NI; ++i) {
+    const int row = t0 + r + L::RG * i;
     // Rows past `limit` are masked before their values are used.
     raw.vs[i] = (row & 1) ? wvs[i] >> 16 : wvs[i] & 0xffffu;
     raw.vz[i] = (row & 1) ? wvz[i] >> 16 : wvz[i] & 0xffffu;
@@ -219,7 +240,7 @@ __device__ __forceinline__ void load_raw(const Src& s, int bs, int block, int h,
 template <int D, int MT>
 struct Widen {
   using Raw = RawModel<D, MT>;
-  static constexpr int EPL = D / 16;
+  static constexpr int EPL = Lanes<D>::EPL;
   __device__ __forceinline__ explicit Widen(const Raw&) {}
   __device__ __forceinline__ static float elem(const uint32_t* w, int e) {
     if constexpr (MT == LKV_F32) {
@@ -243,7 +264,7 @@ struct Widen {
 template <int D, int MT>
 struct WidenI8 {
   using Raw = RawI8<D>;
-  static constexpr int EPL = D / 16;
+  static constexpr int EPL = Lanes<D>::EPL;
   float ks[EPL], kz[EPL];
   __device__ __forceinline__ explicit WidenI8(const Raw& raw) {
 #pragma unroll
@@ -271,18 +292,20 @@ template <int D, int G>
 struct WaveState {
   float m[G];
   float l[G];
-  float o[G][D / 16];
+  float o[G][Lanes<D>::EPL];
 };
 
 // Fold one chunk into the wave's running softmax. `limit`: valid tokens of this pair. Rows are
 // widened one at a time from the raw registers (scores first, then the weighted values).
 template <int D, int G, typename W, typename Raw>
-__device__ __forceinline__ void consume_chunk(const float (&q)[G][D / 16], const W& wd, const Raw& raw, int t0, int nit,
+__device__ __forceinline__ void consume_chunk(const float (&q)[G][Lanes<D>::EPL], const W& wd, const Raw& raw, int t0, int nit,
                                               int limit, int r, WaveState<D, G>& st) {
-  constexpr int EPL = D / 16;
-  float s[4][G];
+  using L = Lanes<D>;
+  constexpr int EPL = L::EPL;
+  constexpr int NI = L::NI;
+  float s[NI][G];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NI; ++i) {
     float x[EPL];
     wd.key(raw, i, x);
 #pragma unroll
@@ -290,26 +313,26 @@ __device__ __forceinline__ void consume_chunk(const float (&q)[G][D / 16], const
       float acc = 0.0f;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) acc = fmaf(q[j][e], x[e], acc);
-      s[i][j] = lkv::row16_sum(acc);
+      s[i][j] = lkv::row_sum<L::LPR>(acc);
     }
   }
-  bool valid[4];
+  bool valid[NI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) valid[i] = i < nit && (t0 + r + 4 * i) < limit;
-  float p[4][G];
+  for (int i = 0; i < NI; ++i) valid[i] = i < nit && (t0 + r + L::RG * i) < limit;
+  float p[NI][G];
   bool live[G];
 #pragma unroll
   for (int j = 0; j < G; ++j) {
     float cm = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) cm = valid[i] ? fmaxf(cm, s[i][j]) : cm;
-    cm = lkv::groups4_max(cm);
+    for (int i = 0; i < NI; ++i) cm = valid[i] ? fmaxf(cm, s[i][j]) : cm;
+    cm = lkv::groups_max<L::RG>(cm);
     const float m_new = fmaxf(st.m[j], cm);
     live[j] = m_new != -INFINITY;  // wave-uniform; false while nothing valid has been seen
     const float alpha = live[j] ? exp2f(st.m[j] - m_new) : 1.0f;  // exp2(-inf) = 0 on the first valid chunk
     float psum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NI; ++i) {
       p[i][j] = (valid[i] && live[j]) ? exp2f(s[i][j] - m_new) : 0.0f;
       psum += p[i][j];
     }
@@ -321,7 +344,7 @@ __device__ __forceinline__ void consume_chunk(const float (&q)[G][D / 16], const
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NI; ++i) {
     if (!valid[i]) continue;  // masked rows may hold non-finite data
     float x[EPL];
     wd.value(raw, i, x);
@@ -352,13 +375,13 @@ __device__ __forceinline__ void load_pair_raw(const Src& s, int bs, bool ok, int
 // `block_b` < 0: a single pair. Ids outside the source are skipped (wave-uniform), never read.
 template <int D, int MT, int G, typename Raw>
 __device__ __forceinline__ void process_two(const DecodeArgs& a, const Src& s, int block_a, int block_b, int h,
-                                            int limit, const float (&q)[G][D / 16], int r, int c,
+                                            int limit, const float (&q)[G][Lanes<D>::EPL], int r, int c,
                                             WaveState<D, G>& st) {
   const bool ok_a = block_a >= 0 && (int64_t)block_a < s.nblk;
   const bool ok_b = kPairs<G> == 2 && block_b >= 0 && (int64_t)block_b < s.nblk;
 #pragma unroll 1
   for (int t0 = 0; t0 < a.bs; t0 += 16) {
-    const int nit = min(4, (a.bs - t0) >> 2);
+    const int nit = min(Lanes<D>::NI, (a.bs - t0 + Lanes<D>::RG - 1) / Lanes<D>::RG);
     using Wd = typename std::conditional<std::is_same<Raw, RawI8<D>>::value, WidenI8<D, MT>, Widen<D, MT>>::type;
     Raw ra;
     if constexpr (kPairs<G> == 2) {
@@ -378,7 +401,7 @@ __device__ __forceinline__ void process_two(const DecodeArgs& a, const Src& s, i
 // the model-dtype kernels' register use down (512-thread workgroups leave no spill registers).
 template <int D, int MT, int G, bool I8>
 __device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, int block_a, int block_b, int h,
-                                           int limit, const float (&q)[G][D / 16], int r, int c,
+                                           int limit, const float (&q)[G][Lanes<D>::EPL], int r, int c,
                                            WaveState<D, G>& st) {
   if constexpr (I8) {
     if (s.dtype == LKV_INT8_RECORD) {
@@ -393,15 +416,15 @@ __device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, in
 // chunk it loads into `slot` of the slot pool (model-dtype sources; int8 records take
 // attend_fill_i8). The same loads and arithmetic as the zero-copy path, so the result is identical.
 template <int D, int MT, int G>
-__device__ __forceinline__ void attend_fill(const DecodeArgs& a, int block, int slot, int h, const float (&q)[G][D / 16],
+__device__ __forceinline__ void attend_fill(const DecodeArgs& a, int block, int slot, int h, const float (&q)[G][Lanes<D>::EPL],
                                             int r, int c, WaveState<D, G>& st) {
   if (block < 0 || (int64_t)block >= a.sel.nblk || slot < 0 || (int64_t)slot >= a.slots.nblk) return;  // wave-uniform
 #pragma unroll 1
   for (int t0 = 0; t0 < a.bs; t0 += 16) {
-    const int nit = min(4, (a.bs - t0) >> 2);
+    const int nit = min(Lanes<D>::NI, (a.bs - t0 + Lanes<D>::RG - 1) / Lanes<D>::RG);
     RawModel<D, MT> raw;
     load_raw<D, MT>(a.sel, block, h, t0, nit, a.bs, r, c, raw);
-    store_raw<D, MT>(a.slots, slot, h, t0, nit, r, c, raw);
+    store_raw<D, MT>(a.slots, slot, h, t0, nit, a.bs, r, c, raw);
     consume_chunk<D, G>(q, Widen<D, MT>(raw), raw, t0, nit, a.bs, r, st);
   }
 }
@@ -410,24 +433,25 @@ __device__ __forceinline__ void attend_fill(const DecodeArgs& a, int block, int 
 // path does, its rows -- model-dtype values -- are written into `slot`, and the chunk is attended.
 // A later hit reads back exactly these values, so hits and misses attend the same numbers.
 template <int D, int MT, int G>
-__device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, int slot, int h, const float (&q)[G][D / 16],
+__device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, int slot, int h, const float (&q)[G][Lanes<D>::EPL],
                                                int r, int c, WaveState<D, G>& st) {
   using T = typename lkv::Elem<MT>::T;
-  constexpr int EPL = D / 16;
+  using L = Lanes<D>;
+  constexpr int EPL = L::EPL;
   if (block < 0 || (int64_t)block >= a.sel.nblk || slot < 0 || (int64_t)slot >= a.slots.nblk) return;  // wave-uniform
   const int64_t off = (int64_t)slot * a.slots.bstride + (int64_t)h * a.slots.hstride + c * EPL;
   T* kb = (T*)a.slots.k + off;
   T* vb = (T*)a.slots.v + off;
 #pragma unroll 1
   for (int t0 = 0; t0 < a.bs; t0 += 16) {
-    const int nit = min(4, (a.bs - t0) >> 2);
+    const int nit = min(Lanes<D>::NI, (a.bs - t0 + Lanes<D>::RG - 1) / Lanes<D>::RG);
     RawI8<D> raw;
     load_raw<D>(a.sel, a.bs, block, h, t0, nit, a.bs, r, c, raw);
     const WidenI8<D, MT> wd(raw);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i < nit) {
-        const int row = t0 + r + 4 * i;
+    for (int i = 0; i < L::NI; ++i) {
+      const int row = t0 + r + L::RG * i;
+      if (i < nit && row < a.bs) {  // rows of a short last chunk past the block are not written
         float x[EPL];
         T t[EPL];
         wd.key(raw, i, x);
@@ -446,12 +470,13 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
 
 template <int D, int MT, int G, int NT, bool I8>
 __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
+  using L = Lanes<D>;
   constexpr int NW = NT / 64;
-  constexpr int EPL = D / 16;
+  constexpr int EPL = L::EPL;
   const int h = blockIdx.x % a.n_kv;
   const int split = blockIdx.x / a.n_kv;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane >> 4, c = lane & 15;
+  const int r = lane / L::LPR, c = lane % L::LPR;  // row group, lane within the row
   const int S = a.splits_a + a.splits_b;
 
   __shared__ float s_m[NW][G], s_l[NW][G];
@@ -542,9 +567,9 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   // ---- wave totals: sum the four row groups, then combine the waves in LDS ---------------------
 #pragma unroll
   for (int j = 0; j < G; ++j) {
-    const float l = lkv::groups4_sum(st.l[j]);
+    const float l = lkv::groups_sum<L::RG>(st.l[j]);
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) st.o[j][e] = lkv::groups4_sum(st.o[j][e]);
+    for (int e = 0; e < EPL; ++e) st.o[j][e] = lkv::groups_sum<L::RG>(st.o[j][e]);
     if (lane == 0) {
       s_m[wave][j] = st.m[j];
       s_l[wave][j] = l;
