@@ -8,8 +8,35 @@ unused rows (lazykv/cache.py:1-9,34-54). Batch size 1 only, as in the reference.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 from transformers.cache_utils import Cache, CacheLayerMixin
+
+
+@dataclass
+class Decoded:
+    """What a selector's `select` returns here (TieredCache, QuestView): the finished attention of
+    the step, not a key set. out [1, n_q, 1, d] in the model dtype, lse [1, n_q] float32 (natural log)."""
+
+    out: torch.Tensor
+    lse: torch.Tensor
+
+
+@dataclass
+class CacheStats:
+    """Where a cache's KV lives (lazykv/cache.py:105-115): bytes resident in VRAM, bytes held only
+    in host memory, and the VRAM allocated for KV."""
+
+    seq_len: int
+    gpu_resident_kv_bytes: int
+    host_kv_bytes: int
+    gpu_allocated_kv_bytes: int
+
+    @property
+    def gpu_residency_fraction(self) -> float:
+        total = self.gpu_resident_kv_bytes + self.host_kv_bytes
+        return 1.0 if total == 0 else self.gpu_resident_kv_bytes / total
 
 
 class PreallocatedLayer(CacheLayerMixin):
@@ -58,6 +85,13 @@ class PreallocatedLayer(CacheLayerMixin):
             raise ValueError(f"cannot truncate length {self.length} to {length}")
         self.length = length
 
+    def resident_bytes(self) -> int:
+        """KV bytes of the filled prefix (lazykv/cache.py:73-77)."""
+        if not self.is_initialized:
+            return 0
+        per_token = self.keys[0, :, 0].numel() * self.keys.element_size() + self.values[0, :, 0].numel() * self.values.element_size()
+        return per_token * self.length
+
 
 class FullGPUCache(Cache):
     """Every layer's KV resident on the GPU, preallocated (lazykv/cache.py:72-80)."""
@@ -69,6 +103,15 @@ class FullGPUCache(Cache):
     def truncate(self, length: int) -> None:
         for layer in self.layers:
             layer.truncate(length)
+
+    def stats(self) -> CacheStats:
+        """Everything resident (lazykv/cache.py:91-102)."""
+        layers = [layer for layer in self.layers if isinstance(layer, PreallocatedLayer)]
+        resident = sum(layer.resident_bytes() for layer in layers)
+        allocated = sum(layer.keys.numel() * layer.keys.element_size() + layer.values.numel() * layer.values.element_size()
+                        for layer in layers if layer.is_initialized)
+        return CacheStats(seq_len=layers[0].get_seq_length() if layers else 0, gpu_resident_kv_bytes=resident, host_kv_bytes=0,
+                          gpu_allocated_kv_bytes=allocated)
 
     @classmethod
     def from_kv(cls, layers: list[tuple[torch.Tensor, torch.Tensor]], max_len: int) -> FullGPUCache:

@@ -35,7 +35,7 @@ import torch
 from transformers.cache_utils import Cache
 
 from lazykv_amd import _lib, kernels
-from lazykv_amd.cache import FullGPUCache
+from lazykv_amd.cache import CacheStats, Decoded, FullGPUCache  # Decoded: what select returns
 from lazykv_amd.pinned import pinned_empty
 from lazykv_amd.quant import packed_pair_bytes
 from lazykv_amd.selection import QUEST_DENSE_LAYERS
@@ -55,17 +55,6 @@ class TierCounters:
     seal_bytes: int = 0
     boundary_d2h_bytes: int = 0
     fetched_pairs_per_step: list[int] = field(default_factory=list)
-
-
-@dataclass
-class Decoded:
-    """What `TieredCache.select` returns: the finished attention of the step, not a key set.
-
-    out [1, n_q, 1, d] in the model dtype, lse [1, n_q] float32 (natural log).
-    """
-
-    out: torch.Tensor
-    lse: torch.Tensor
 
 
 def allocate_host_pools(n_layers: int, heads: int, head_dim: int, block_size: int, capacity_tokens: int, dtype: torch.dtype = torch.bfloat16, quant: str | None = None, coherent: bool = False) -> list[torch.Tensor]:
@@ -333,6 +322,23 @@ class TieredLayer:
     def metadata_bytes(self) -> int:
         return 2 * self.kmin.numel() * self.kmin.element_size()
 
+    def _not_resident_blocks(self) -> int:
+        """Sealed blocks no GPU copy holds, summed over heads: all but the sink (pool slot 0) for a
+        zero-copy tier, none for an HBM store, and those outside the slots for the hybrid tier
+        (read from its table: a host sync, for reporting only)."""
+        if self.store is not None:
+            return 0
+        held = int((self.res.slot_block >= 0).sum().item()) if self.res is not None else 0
+        return max(0, self.h * max(0, self.n_sealed - 1) - held)
+
+    def not_resident_bytes(self) -> int:
+        """Host bytes of blocks VRAM does not hold, in the tier's storage format (lazykv/tiered.py:845-847)."""
+        return self._not_resident_blocks() * self.pair_bytes
+
+    def not_resident_logical_bytes(self) -> int:
+        """The same blocks in the model dtype (lazykv/tiered.py:850-857)."""
+        return self._not_resident_blocks() * self.logical_pair_bytes
+
     def host_bytes(self) -> int:
         return self.n_sealed * self.h * self.pair_bytes if self.host is not None else 0
 
@@ -439,6 +445,22 @@ class TieredCache(Cache):
 
     def close(self) -> None:
         pass
+
+    def stats(self) -> CacheStats:
+        """VRAM held for decode (dense layers' KV, slot pools, stores, metadata) and host bytes no
+        GPU copy holds, so gpu / (gpu + host) is the residency fraction (lazykv/tiered.py:841-848)."""
+        dense = sum(self.full.layers[i].resident_bytes() for i in range(len(self.full.layers)) if i not in self.tiers)
+        gpu = dense + sum(t.gpu_bytes() + t.metadata_bytes() for t in self.tiers.values())
+        host = sum(t.not_resident_bytes() for t in self.tiers.values())
+        return CacheStats(seq_len=self.get_seq_length(self.dense_layers), gpu_resident_kv_bytes=gpu, host_kv_bytes=host, gpu_allocated_kv_bytes=gpu)
+
+    def host_logical_bytes(self) -> int:
+        """What the off-GPU KV would occupy in the model dtype, whatever precision the tier stores
+        it in (lazykv/tiered.py:850-857): stats().host_kv_bytes over this is the int8 saving."""
+        return sum(t.not_resident_logical_bytes() for t in self.tiers.values())
+
+    def host_pinned_bytes(self) -> int:
+        return sum(t.host.numel() * t.host.element_size() for t in self.tiers.values() if t.host is not None)
 
     def counters_dict(self) -> dict[str, Any]:
         from dataclasses import asdict
