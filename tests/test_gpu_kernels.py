@@ -487,3 +487,22 @@ def test_pinned_pool_round_trips_and_the_stream_probe_reads_it() -> None:
     kernels.stream_read(d.data_ptr(), d.numel(), 64, sink_dev)
     torch.cuda.synchronize()
     assert torch.equal(sink, sink_dev) and sink.abs().sum() > 0
+
+
+def test_install_verifies_the_decode_kernel_and_refuses_unknown_strategies() -> None:
+    """install() with the model's head counts checks decode (the HIP kernel, spare storage past the
+    live length) and chunked prefill against the float32 truth first (lazykv/attention.py:214-290);
+    a strategy this build does not have is a hard error."""
+    from lazykv_amd import attention
+
+    chosen, checks = attention.install(None, 32, 8, 128)
+    assert chosen == "hip" and len(checks) == 1 and checks[0].ok, checks
+    assert checks[0].max_rel_err_decode < 1e-2 and checks[0].max_rel_err_prefill < 1e-2
+    assert checks[0].seconds_decode_growing_median > 0
+    assert attention.current_strategy() == ("hip", 0)
+    chosen, checks = attention.install("hip", 32, 8, 64)
+    assert checks[0].ok, checks
+    with pytest.raises(RuntimeError, match="failed verification"):
+        attention.install("cudnn", 32, 8, 64)
+    with pytest.raises(RuntimeError, match="unknown attention strategy"):
+        attention.install("math")
