@@ -273,11 +273,6 @@ __device__ __forceinline__ float row_sum(float x) {
 // Combine the four 16-lane row groups of a wave (lanes l, l^16, l^32, l^48).
 __device__ __forceinline__ float xor_lane(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
-__device__ __forceinline__ float groups4_sum(float x) {
-  x += xor_lane(x, 16);
-  x += xor_lane(x, 32);
-  return x;
-}
 __device__ __forceinline__ float groups4_max(float x) {
   x = fmaxf(x, xor_lane(x, 16));
   x = fmaxf(x, xor_lane(x, 32));
