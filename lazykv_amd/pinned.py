@@ -15,22 +15,26 @@ from __future__ import annotations
 
 import bisect
 import ctypes
+import threading
 import weakref
 
 import torch
 
 from lazykv_amd import _lib
 
-# Live allocations: sorted host base addresses -> (nbytes, device base address).
+# Live allocations: sorted host base addresses -> (nbytes, device base address). Finalizers may
+# run on any thread, so every read and update holds the lock.
 _BASES: list[int] = []
 _ALLOCS: dict[int, tuple[int, int]] = {}
+_LOCK = threading.Lock()
 
 
 def _free(ptr: int) -> None:
-    i = bisect.bisect_left(_BASES, ptr)
-    if i < len(_BASES) and _BASES[i] == ptr:
-        _BASES.pop(i)
-        _ALLOCS.pop(ptr, None)
+    with _LOCK:
+        i = bisect.bisect_left(_BASES, ptr)
+        if i < len(_BASES) and _BASES[i] == ptr:
+            _BASES.pop(i)
+            _ALLOCS.pop(ptr, None)
     try:
         _lib.lib().lkv_host_free(ptr)
     except Exception:  # noqa: BLE001 -- at interpreter exit the runtime may already be gone
@@ -53,8 +57,9 @@ def pinned_empty(shape: tuple[int, ...], dtype: torch.dtype, coherent: bool = Fa
     _lib.check(_lib.lib().lkv_host_device_pointer(host, ctypes.byref(dev)), "device address of the host pool")
     buf = (ctypes.c_uint8 * nbytes).from_address(host)
     t = torch.frombuffer(buf, dtype=torch.uint8, count=nbytes).view(dtype).view(shape)
-    bisect.insort(_BASES, host)
-    _ALLOCS[host] = (nbytes, int(dev.value))
+    with _LOCK:
+        bisect.insort(_BASES, host)
+        _ALLOCS[host] = (nbytes, int(dev.value))
     # Tied to the buffer object, which the tensor's storage (shared by every view) keeps alive:
     # the memory is released only when the last view is gone.
     weakref.finalize(buf, _free, host)
@@ -64,12 +69,13 @@ def pinned_empty(shape: tuple[int, ...], dtype: torch.dtype, coherent: bool = Fa
 def device_address(t: torch.Tensor) -> int:
     """The device address of the first element of a CPU tensor that lives in a pinned_empty pool."""
     ptr = t.data_ptr()
-    i = bisect.bisect_right(_BASES, ptr) - 1
-    if i >= 0:
-        base = _BASES[i]
-        nbytes, dev = _ALLOCS[base]
-        if ptr < base + nbytes:
-            return dev + (ptr - base)
+    with _LOCK:
+        i = bisect.bisect_right(_BASES, ptr) - 1
+        if i >= 0:
+            base = _BASES[i]
+            nbytes, dev = _ALLOCS[base]
+            if ptr < base + nbytes:
+                return dev + (ptr - base)
     raise ValueError("tensor is not in memory from pinned_empty; the device cannot read it in place")
 
 
