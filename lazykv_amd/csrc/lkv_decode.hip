@@ -355,8 +355,9 @@ __device__ __forceinline__ void consume_chunk(const float (&q)[G][Lanes<D>::EPL]
   }
 }
 
-// Pairs a wave keeps in flight. Measured at the 8B shape (bf16, d = 128, G = 4), one pair per
-// wave at a time (and so more waves resident) beats two for both HBM and host-memory sources.
+// Pairs a wave keeps in flight in the remainder segment: one (measured on runs of consecutive
+// blocks from HBM and from host memory, two were no faster). The selected segment takes two in
+// kernels without int8 code (see the kernel), one otherwise.
 template <int G>
 constexpr int kPairs = 1;
 
@@ -373,18 +374,18 @@ __device__ __forceinline__ void load_pair_raw(const Src& s, int bs, bool ok, int
 
 // Attend up to two pairs of one source: both pairs' loads are issued before either is consumed.
 // `block_b` < 0: a single pair. Ids outside the source are skipped (wave-uniform), never read.
-template <int D, int MT, int G, typename Raw>
+template <int D, int MT, int G, typename Raw, int NP>
 __device__ __forceinline__ void process_two(const DecodeArgs& a, const Src& s, int block_a, int block_b, int h,
                                             int limit, const float (&q)[G][Lanes<D>::EPL], int r, int c,
                                             WaveState<D, G>& st) {
   const bool ok_a = block_a >= 0 && (int64_t)block_a < s.nblk;
-  const bool ok_b = kPairs<G> == 2 && block_b >= 0 && (int64_t)block_b < s.nblk;
+  const bool ok_b = NP == 2 && block_b >= 0 && (int64_t)block_b < s.nblk;
 #pragma unroll 1
   for (int t0 = 0; t0 < a.bs; t0 += 16) {
     const int nit = min(Lanes<D>::NI, (a.bs - t0 + Lanes<D>::RG - 1) / Lanes<D>::RG);
     using Wd = typename std::conditional<std::is_same<Raw, RawI8<D>>::value, WidenI8<D, MT>, Widen<D, MT>>::type;
     Raw ra;
-    if constexpr (kPairs<G> == 2) {
+    if constexpr (NP == 2) {
       Raw rb;
       load_pair_raw<D, MT>(s, a.bs, ok_a, block_a, h, t0, nit, limit, r, c, ra);
       load_pair_raw<D, MT>(s, a.bs, ok_b, block_b, h, t0, nit, limit, r, c, rb);
@@ -399,17 +400,17 @@ __device__ __forceinline__ void process_two(const DecodeArgs& a, const Src& s, i
 
 // I8: the launch may read int8 records. Without it the int8 code is not compiled in, which keeps
 // the model-dtype kernels' register use down (512-thread workgroups leave no spill registers).
-template <int D, int MT, int G, bool I8>
+template <int D, int MT, int G, bool I8, int NP = 1>
 __device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, int block_a, int block_b, int h,
                                            int limit, const float (&q)[G][Lanes<D>::EPL], int r, int c,
                                            WaveState<D, G>& st) {
   if constexpr (I8) {
     if (s.dtype == LKV_INT8_RECORD) {
-      process_two<D, MT, G, RawI8<D>>(a, s, block_a, block_b, h, limit, q, r, c, st);
+      process_two<D, MT, G, RawI8<D>, NP>(a, s, block_a, block_b, h, limit, q, r, c, st);
       return;
     }
   }
-  process_two<D, MT, G, RawModel<D, MT>>(a, s, block_a, block_b, h, limit, q, r, c, st);
+  process_two<D, MT, G, RawModel<D, MT>, NP>(a, s, block_a, block_b, h, limit, q, r, c, st);
 }
 
 // A residency miss: attend `block` of the host source exactly as attend_two does, and copy each
@@ -512,27 +513,30 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     const int js = max(first, has_sink) - has_sink;
     const int je = min(last, has_sink + n_sel) - has_sink;
     const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
-    static_assert(kPairs<G> == 1, "the hybrid path below attends one pair per wave per round");
-    for (int j = js + wave; j < je; j += kPairs<G> * NW) {
+    // Instances without int8 code never run the hybrid branch (hybrid launches take the general
+    // instance) and keep two selected pairs in flight per wave: with about two items per wave in
+    // the HBM plan, both loads are issued before either is consumed (config-0 shape 16.2 -> 15.4
+    // us, identical results). The others, and float32 pools (which would spill), keep one.
+    constexpr int NPA = (I8 || MT == LKV_F32) ? 1 : 2;
+    for (int j = js + wave; j < je; j += NPA * NW) {
       const int b0 = idx_h[j];
-      if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
-        const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
-        if (l >= 0 && (l & kLocMiss)) {
-          bool filled = false;
-          if constexpr (I8) {
+      if constexpr (I8) {
+        if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
+          const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
+          if (l >= 0 && (l & kLocMiss)) {
             if (a.sel.dtype == LKV_INT8_RECORD) {
               attend_fill_i8<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
-              filled = true;
+            } else {
+              attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
             }
+          } else if (l >= 0) {
+            attend_two<D, MT, G, I8>(a, a.slots, l, -1, h, a.bs, q, r, c, st);
           }
-          if (!filled) attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
-        } else if (l >= 0) {
-          attend_two<D, MT, G, I8>(a, a.slots, l, -1, h, a.bs, q, r, c, st);
+          continue;
         }
-        continue;
       }
-      const int b1 = (kPairs<G> == 2 && j + NW < je) ? idx_h[j + NW] : -1;
-      attend_two<D, MT, G, I8>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
+      const int b1 = (NPA == 2 && j + NW < je) ? idx_h[j + NW] : -1;
+      attend_two<D, MT, G, I8, NPA>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
     }
   } else {
     // Segment B: remainder blocks of this run that idx does not name.
@@ -765,8 +769,9 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
 template <int D, int MT, int G>
 int launch(hipStream_t stream, DecodeArgs& a) {
   const int S = a.splits_a + a.splits_b;
+  // The general instance (int8 code, the hybrid branch) for int8 sources and hybrid launches.
   const bool i8 = a.sel.dtype == LKV_INT8_RECORD || a.rem.dtype == LKV_INT8_RECORD || a.sink.dtype == LKV_INT8_RECORD ||
-                  a.cur.dtype == LKV_INT8_RECORD;
+                  a.cur.dtype == LKV_INT8_RECORD || a.loc != nullptr;
   bool launched = false;
   if constexpr (G <= 4) {
     if (a.nt == kThreadsHbm) {
