@@ -513,14 +513,16 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     const int js = max(first, has_sink) - has_sink;
     const int je = min(last, has_sink + n_sel) - has_sink;
     const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
-    // Instances without int8 code never run the hybrid branch (hybrid launches take the general
-    // instance) and keep two selected pairs in flight per wave: with about two items per wave in
-    // the HBM plan, both loads are issued before either is consumed (config-0 shape 16.2 -> 15.4
-    // us, identical results). The others, and float32 pools (which would spill), keep one.
-    constexpr int NPA = (I8 || MT == LKV_F32) ? 1 : 2;
+    // The hybrid branch is compiled only into the 4-wave general instance, which every hybrid
+    // launch takes. The other instances keep two selected pairs in flight per wave: with about two
+    // items per wave in the HBM plan, both loads are issued before either is consumed (config-0
+    // shape 16.2 -> 15.4 us, int8 records in HBM 24.4 -> 23.5 us, identical results). Float32
+    // pools keep one (two would spill).
+    constexpr bool HYB = I8 && NT == kThreads;
+    constexpr int NPA = (HYB || MT == LKV_F32) ? 1 : 2;
     for (int j = js + wave; j < je; j += NPA * NW) {
       const int b0 = idx_h[j];
-      if constexpr (I8) {
+      if constexpr (HYB) {
         if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
           const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
           if (l >= 0 && (l & kLocMiss)) {
@@ -769,7 +771,8 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
 template <int D, int MT, int G>
 int launch(hipStream_t stream, DecodeArgs& a) {
   const int S = a.splits_a + a.splits_b;
-  // The general instance (int8 code, the hybrid branch) for int8 sources and hybrid launches.
+  // Instances with int8 code for int8 sources; hybrid launches take the 4-wave one (the only one
+  // with the hybrid branch).
   const bool i8 = a.sel.dtype == LKV_INT8_RECORD || a.rem.dtype == LKV_INT8_RECORD || a.sink.dtype == LKV_INT8_RECORD ||
                   a.cur.dtype == LKV_INT8_RECORD || a.loc != nullptr;
   bool launched = false;
@@ -780,6 +783,8 @@ int launch(hipStream_t stream, DecodeArgs& a) {
       if (!i8) {
         hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
         launched = true;
+      } else if (a.loc != nullptr) {
+        // hybrid: the 4-wave general instance below
       } else if constexpr (!(D == 128 && G == 4)) {
         hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, true>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
         launched = true;
