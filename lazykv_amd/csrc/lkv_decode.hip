@@ -293,6 +293,7 @@ struct WaveState {
   float m[G];
   float l[G];
   float o[G][Lanes<D>::EPL];
+  float mh;  // matrix-core path: m of head lane % 16 (that lane's copy of m[lane % 16])
 };
 
 // Fold one chunk into the wave's running softmax. `limit`: valid tokens of this pair. Rows are
@@ -413,6 +414,229 @@ __device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, in
   process_two<D, MT, G, RawModel<D, MT>, NP>(a, s, block_a, block_b, h, limit, q, r, c, st);
 }
 
+// ---- Q.K on the matrix cores ---------------------------------------------------------------------
+// The 8-wave model-dtype instances score a 16-token chunk with one v_mfma_f32_16x16x32 per 32
+// channels: A = the chunk's 16 key rows (lane l: row l % 16, channels 32s + 8 (l / 16) .. + 7),
+// B = the query rows of the KV head's G query heads, in the model dtype as given (lane l: head
+// l % 16, zero for heads >= G), D = scores (lane l: rows 4 (l / 16) + i, i < 4, of head l % 16).
+// Products of two model-dtype values are exact in float32 and are summed in float32, as in the
+// vector path; the softmax scale multiplies the sum. The online softmax of a head runs in the
+// lanes that hold its scores; the weights p, and each head's new maximum, rescale factor and
+// weight sum, reach the other lanes through a small per-wave LDS area, and P.V stays on the
+// vector ALUs in the layout of consume_chunk.
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+template <int MT>
+struct Mfma;
+template <>
+struct Mfma<LKV_BF16> {
+  typedef __attribute__((ext_vector_type(8))) __bf16 V8;
+  __device__ __forceinline__ static f32x4 mma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+};
+template <>
+struct Mfma<LKV_F16> {
+  typedef __attribute__((ext_vector_type(8))) _Float16 V8;
+  __device__ __forceinline__ static f32x4 mma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+};
+
+// Floats of a wave's LDS broadcast area for up to NP pairs per step: p[NP][16][G], then the rows
+// m_new[G], alpha[G], psum[G].
+template <int G, int NP>
+constexpr int kMfBroadcast = (16 * NP + 3) * G;
+constexpr int kMfMaxPairs = 3;
+
+// The B operands: lane l holds channels 32s + 8 (l / 16) .. + 7 of query head l % 16 (the query
+// row is 16-byte aligned, which the launch checks).
+template <int D, int MT, int G>
+__device__ __forceinline__ void load_query_mf(const void* q, int h, int lane, typename Mfma<MT>::V8 (&qb)[D / 32]) {
+  const int j = lane % 16;
+  const uint16_t* row = (const uint16_t*)q + ((int64_t)h * G + (j < G ? j : 0)) * D + 8 * (lane / 16);
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) {
+    uint4 x = *(const uint4*)(row + 32 * s);  // heads past G read head 0's row and are zeroed
+    if (j >= G) x = make_uint4(0u, 0u, 0u, 0u);
+    qb[s] = __builtin_bit_cast(typename Mfma<MT>::V8, x);
+  }
+}
+
+// One chunk of a pair: keys in the MFMA layout, values as load_raw lays them out.
+template <int D, int MT>
+struct RawMf {
+  typename Mfma<MT>::V8 k[D / 32];
+  uint32_t v[Lanes<D>::NI][RawModel<D, MT>::W];
+};
+
+template <int D, int MT>
+__device__ __forceinline__ void load_raw_mf(const Src& s, int block, int h, int t0, int nit, int limit, int lane, int r, int c,
+                                            RawMf<D, MT>& raw) {
+  using L = Lanes<D>;
+  constexpr int EPL = L::EPL;
+  const int64_t base = (int64_t)block * s.bstride + (int64_t)h * s.hstride;
+  const uint16_t* kb = (const uint16_t*)s.k + base;
+  const uint16_t* vb = (const uint16_t*)s.v + base;
+  // A key row past `limit` reads the block's row 0 instead; its score is masked before use.
+  const int kr = t0 + lane % 16;
+  const uint16_t* krow = kb + (int64_t)(kr < limit ? kr : 0) * D + 8 * (lane / 16);
+#pragma unroll
+  for (int st = 0; st < D / 32; ++st) raw.k[st] = __builtin_bit_cast(typename Mfma<MT>::V8, *(const uint4*)(krow + 32 * st));
+#pragma unroll
+  for (int i = 0; i < L::NI; ++i) {
+    const int row = t0 + r + L::RG * i;
+    const bool ok = i < nit && row < limit;
+    load_words(vb + (int64_t)(ok ? row : 0) * D + c * EPL, raw.v[i]);
+#pragma unroll
+    for (int w = 0; w < RawModel<D, MT>::W; ++w) raw.v[i][w] = ok ? raw.v[i][w] : 0u;
+  }
+}
+
+// Fold the same chunk (rows t0 .. t0 + 15) of NP pairs into the wave's running softmax, as
+// consume_chunk does one pair at a time, with the scores from the matrix cores: one maximum, one
+// rescale and one broadcast for all NP pairs. lim[u]: valid tokens of pair u (0 skips the pair).
+// `sp`: this wave's broadcast area.
+template <int D, int MT, int G, int NP>
+__device__ __forceinline__ void consume_mf(const typename Mfma<MT>::V8 (&qb)[D / 32], const RawMf<D, MT> (&raw)[NP], float qscale,
+                                           int t0, int nit, const int (&lim)[NP], int lane, int r, float* sp, WaveState<D, G>& st) {
+  using L = Lanes<D>;
+  constexpr int EPL = L::EPL;
+  const int j = lane % 16, lg = lane / 16;
+  f32x4 acc[NP];
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    acc[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (lim[u] > 0) {  // wave-uniform
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) acc[u] = Mfma<MT>::mma(raw[u].k[s], qb[s], acc[u]);
+    }
+  }
+  float sc[NP][4];
+  bool vld[NP][4];
+  float cm = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < NP; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[u][i] = acc[u][i] * qscale;
+      vld[u][i] = t0 + 4 * lg + i < lim[u];
+      cm = vld[u][i] ? fmaxf(cm, sc[u][i]) : cm;
+    }
+  cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+  cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+  const float m_old = st.mh;
+  const float m_new = fmaxf(m_old, cm);
+  const bool live = m_new != -INFINITY;  // false while nothing valid has been seen
+  const float alpha = live ? exp2f(m_old - m_new) : 1.0f;
+  float p[NP][4];
+  float ps = 0.0f;
+#pragma unroll
+  for (int u = 0; u < NP; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[u][i] = (vld[u][i] && live) ? exp2f(sc[u][i] - m_new) : 0.0f;
+      ps += p[u][i];
+    }
+  ps += __shfl_xor(ps, 16, 64);
+  ps += __shfl_xor(ps, 32, 64);
+  st.mh = live ? m_new : m_old;
+  if (j < G) {
+#pragma unroll
+    for (int u = 0; u < NP; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sp[(16 * u + 4 * lg + i) * G + j] = p[u][i];
+    if (lg == 0) {
+      sp[(16 * NP) * G + j] = m_new;
+      sp[(16 * NP + 1) * G + j] = alpha;
+      sp[(16 * NP + 2) * G + j] = ps;
+    }
+  }
+  // LDS operations of one wave complete in order: the wave's reads below see its writes above.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int jj = 0; jj < G; ++jj) {
+    const float mn = sp[(16 * NP) * G + jj], al = sp[(16 * NP + 1) * G + jj], pj = sp[(16 * NP + 2) * G + jj];
+    if (mn != -INFINITY) {
+      st.m[jj] = mn;
+      st.l[jj] = st.l[jj] * al + (r == 0 ? pj : 0.0f);  // the step's sum counts once over the row groups
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) st.o[jj][e] *= al;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NP; ++u)
+#pragma unroll
+    for (int i = 0; i < L::NI; ++i) {
+      const int row = r + L::RG * i;
+      if (!(i < nit && t0 + row < lim[u])) continue;  // masked rows may hold non-finite data
+      float pr[G];
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj) pr[jj] = sp[(16 * u + row) * G + jj];
+      float x[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) x[e] = Widen<D, MT>::elem(raw[u].v[i], e);
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) st.o[jj][e] = fmaf(pr[jj], x[e], st.o[jj][e]);
+    }
+  // The next step rewrites the area only after these reads (in order, as above).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Item j0 + u * NW (u < NP) of a segment-A run [.., last): the sink is item 0 when present, the
+// current block the last item (n_a - 1) when present, and the items between are the selected ids in
+// idx order. An item past the run gets block -1 (skipped). Wave-uniform; the ids are read into
+// scalar registers.
+template <int NP, int NW>
+__device__ __forceinline__ void segment_items(const DecodeArgs& a, const int32_t* idx_h, int j0, int last, Src (&s)[NP],
+                                              int (&blk)[NP], int (&lim)[NP]) {
+  const int has_sink = a.sink_block >= 0;
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const int it = j0 + u * NW;
+    s[u] = a.sel;
+    blk[u] = -1;
+    lim[u] = a.bs;
+    if (it < last) {
+      if (has_sink && it == 0) {
+        s[u] = a.sink;
+        blk[u] = a.sink_block;
+      } else if (a.cur_block >= 0 && it == a.n_a - 1) {
+        s[u] = a.cur;
+        blk[u] = a.cur_block;
+        lim[u] = a.fill;
+      } else {
+        blk[u] = __builtin_amdgcn_readfirstlane(idx_h[it - has_sink]);
+      }
+    }
+  }
+}
+
+// Up to NP pairs on the matrix cores, each of its own source and valid-token limit: every pair's
+// loads are issued before any is consumed, and they are consumed in item order. Ids outside their
+// source are skipped (wave-uniform), never read.
+template <int D, int MT, int G, int NP>
+__device__ __forceinline__ void process_items_mf(const DecodeArgs& a, const Src (&s)[NP], const int (&blk)[NP], const int (&lim)[NP],
+                                                 int h, const typename Mfma<MT>::V8 (&qb)[D / 32], int lane, int r, int c, float* sp,
+                                                 WaveState<D, G>& st) {
+  bool ok[NP];
+#pragma unroll
+  for (int u = 0; u < NP; ++u) ok[u] = blk[u] >= 0 && (int64_t)blk[u] < s[u].nblk;
+  int lk[NP];  // valid tokens per pair; 0 for a skipped pair
+#pragma unroll
+  for (int u = 0; u < NP; ++u) lk[u] = ok[u] ? lim[u] : 0;
+#pragma unroll 1
+  for (int t0 = 0; t0 < a.bs; t0 += 16) {
+    const int nit = min(Lanes<D>::NI, (a.bs - t0 + Lanes<D>::RG - 1) / Lanes<D>::RG);
+    RawMf<D, MT> raw[NP];
+#pragma unroll
+    for (int u = 0; u < NP; ++u)
+      if (ok[u]) load_raw_mf<D, MT>(s[u], blk[u], h, t0, nit, lim[u], lane, r, c, raw[u]);
+    consume_mf<D, MT, G, NP>(qb, raw, a.qscale, t0, nit, lk, lane, r, sp, st);
+  }
+}
+
 // A residency miss: attend `block` of the host source exactly as attend_two does, and copy each
 // chunk it loads into `slot` of the slot pool (model-dtype sources; int8 records take
 // attend_fill_i8). The same loads and arithmetic as the zero-copy path, so the result is identical.
@@ -469,7 +693,8 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
   }
 }
 
-template <int D, int MT, int G, int NT, bool I8>
+// MF: Q.K on the matrix cores (model-dtype instances whose query has the model dtype).
+template <int D, int MT, int G, int NT, bool I8, bool MF = false>
 __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   using L = Lanes<D>;
   constexpr int NW = NT / 64;
@@ -483,6 +708,12 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   __shared__ float s_m[NW][G], s_l[NW][G];
   __shared__ float s_o[NW][G][D];
   __shared__ uint32_t s_excl[64];  // segment B: bitmap of excluded blocks in this run
+  static_assert(!MF || (!I8 && MT != LKV_F32), "the matrix-core path reads model-dtype pairs");
+  __shared__ float s_pb[MF ? NW : 1][MF ? kMfBroadcast<G, kMfMaxPairs> : 1];
+  using V8 = typename Mfma<MT == LKV_F32 ? LKV_F16 : MT>::V8;
+  V8 qb[D / 32];
+  if constexpr (MF) load_query_mf<D, MT, G>(a.q, h, lane, qb);
+  float* sp = s_pb[MF ? wave : 0];
 
   float q[G][EPL];
   lkv::load_query_rows<D, G, EPL>(a.q, a.q_dtype, h, c, q);
@@ -492,6 +723,7 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     for (int e = 0; e < EPL; ++e) q[j][e] *= a.qscale;
 
   WaveState<D, G> st;
+  st.mh = -INFINITY;
 #pragma unroll
   for (int j = 0; j < G; ++j) {
     st.m[j] = -INFINITY;
@@ -506,39 +738,55 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     const int last = min(a.n_a, first + a.per_a);
     const int has_sink = a.sink_block >= 0;
     const int n_sel = a.attend_selected ? a.k : 0;
-    if (has_sink && first == 0 && wave == 0) attend_two<D, MT, G, I8>(a, a.sink, a.sink_block, -1, h, a.bs, q, r, c, st);
-    if (a.cur_block >= 0 && last == a.n_a && wave == NW - 1)
-      attend_two<D, MT, G, I8>(a, a.cur, a.cur_block, -1, h, a.fill, q, r, c, st);
-    // Selected items of this run: idx positions [js, je), two per wave per round.
-    const int js = max(first, has_sink) - has_sink;
-    const int je = min(last, has_sink + n_sel) - has_sink;
-    const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
-    // The hybrid branch is compiled only into the 4-wave general instance, which every hybrid
-    // launch takes. The other instances keep two selected pairs in flight per wave: with about two
-    // items per wave in the HBM plan, both loads are issued before either is consumed (config-0
-    // shape 16.2 -> 15.4 us, int8 records in HBM 24.4 -> 23.5 us, identical results). Float32
-    // pools keep one (two would spill).
-    constexpr bool HYB = I8 && NT == kThreads;
-    constexpr int NPA = (HYB || MT == LKV_F32) ? 1 : 2;
-    for (int j = js + wave; j < je; j += NPA * NW) {
-      const int b0 = idx_h[j];
-      if constexpr (HYB) {
-        if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
-          const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
-          if (l >= 0 && (l & kLocMiss)) {
-            if (a.sel.dtype == LKV_INT8_RECORD) {
-              attend_fill_i8<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
-            } else {
-              attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
-            }
-          } else if (l >= 0) {
-            attend_two<D, MT, G, I8>(a, a.slots, l, -1, h, a.bs, q, r, c, st);
-          }
-          continue;
-        }
+    if constexpr (MF) {
+      // Every item of the run -- the sink, selected ids, the current block -- is a model-dtype
+      // pair, so each wave takes kMfItems of them per round, all loads in flight together: with
+      // about two items per wave in the HBM plan, the wave that holds a third needs no second
+      // round.
+      constexpr int kMfItems = kMfMaxPairs;
+      const int wv = __builtin_amdgcn_readfirstlane(wave);
+      const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
+      for (int j0 = first + wv; j0 < last; j0 += kMfItems * NW) {
+        Src is[kMfItems];
+        int ib[kMfItems], il[kMfItems];
+        segment_items<kMfItems, NW>(a, idx_h, j0, last, is, ib, il);
+        process_items_mf<D, MT, G, kMfItems>(a, is, ib, il, h, qb, lane, r, c, sp, st);
       }
-      const int b1 = (NPA == 2 && j + NW < je) ? idx_h[j + NW] : -1;
-      attend_two<D, MT, G, I8, NPA>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
+    } else {
+      if (has_sink && first == 0 && wave == 0) attend_two<D, MT, G, I8>(a, a.sink, a.sink_block, -1, h, a.bs, q, r, c, st);
+      if (a.cur_block >= 0 && last == a.n_a && wave == NW - 1)
+        attend_two<D, MT, G, I8>(a, a.cur, a.cur_block, -1, h, a.fill, q, r, c, st);
+      // Selected items of this run: idx positions [js, je), two per wave per round.
+      const int js = max(first, has_sink) - has_sink;
+      const int je = min(last, has_sink + n_sel) - has_sink;
+      const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
+      // The hybrid branch is compiled only into the 4-wave general instance, which every hybrid
+      // launch takes. The other instances keep two selected pairs in flight per wave: with about two
+      // items per wave in the HBM plan, both loads are issued before either is consumed (int8
+      // records in HBM 24.4 -> 23.5 us, identical results). Float32 pools keep one (two would
+      // spill).
+      constexpr bool HYB = I8 && NT == kThreads;
+      constexpr int NPA = (HYB || MT == LKV_F32) ? 1 : 2;
+      for (int j = js + wave; j < je; j += NPA * NW) {
+        const int b0 = idx_h[j];
+        if constexpr (HYB) {
+          if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
+            const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
+            if (l >= 0 && (l & kLocMiss)) {
+              if (a.sel.dtype == LKV_INT8_RECORD) {
+                attend_fill_i8<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
+              } else {
+                attend_fill<D, MT, G>(a, b0, l & ~kLocMiss, h, q, r, c, st);
+              }
+            } else if (l >= 0) {
+              attend_two<D, MT, G, I8>(a, a.slots, l, -1, h, a.bs, q, r, c, st);
+            }
+            continue;
+          }
+        }
+        const int b1 = (NPA == 2 && j + NW < je) ? idx_h[j + NW] : -1;
+        attend_two<D, MT, G, I8, NPA>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
+      }
     }
   } else {
     // Segment B: remainder blocks of this run that idx does not name.
@@ -559,14 +807,36 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
     int b = lo + wave;
-    while (b < hi) {
-      int pick[2] = {-1, -1};
-      int have = 0;
-      while (have < kPairs<G> && b < hi) {
-        if (!((s_excl[(b - lo) >> 5] >> ((b - lo) & 31)) & 1u)) pick[have++] = b;
-        b += NW;
+    if constexpr (MF) {
+      // Up to kMfMaxPairs blocks per step, folded into the softmax together.
+      Src rs[kMfMaxPairs];
+      int lim[kMfMaxPairs];
+#pragma unroll
+      for (int u = 0; u < kMfMaxPairs; ++u) {
+        rs[u] = a.rem;
+        lim[u] = a.bs;
       }
-      if (have) attend_two<D, MT, G, I8>(a, a.rem, pick[0], pick[1], h, a.bs, q, r, c, st);
+      while (b < hi) {
+        int pick[kMfMaxPairs];
+#pragma unroll
+        for (int u = 0; u < kMfMaxPairs; ++u) pick[u] = -1;
+        int have = 0;
+        while (have < kMfMaxPairs && b < hi) {
+          if (!((s_excl[(b - lo) >> 5] >> ((b - lo) & 31)) & 1u)) pick[have++] = b;
+          b += NW;
+        }
+        if (have) process_items_mf<D, MT, G, kMfMaxPairs>(a, rs, pick, lim, h, qb, lane, r, c, sp, st);
+      }
+    } else {
+      while (b < hi) {
+        int pick[2] = {-1, -1};
+        int have = 0;
+        while (have < kPairs<G> && b < hi) {
+          if (!((s_excl[(b - lo) >> 5] >> ((b - lo) & 31)) & 1u)) pick[have++] = b;
+          b += NW;
+        }
+        if (have) attend_two<D, MT, G, I8>(a, a.rem, pick[0], pick[1], h, a.bs, q, r, c, st);
+      }
     }
   }
 
@@ -781,7 +1051,15 @@ int launch(hipStream_t stream, DecodeArgs& a) {
       // The int8-capable 512-thread kernel spills at D = 128, G = 4; such a launch takes the
       // 256-thread kernel over the same plan (its waves stride the same runs of items).
       if (!i8) {
-        hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
+        // Q.K on the matrix cores when the query has the model dtype and 16-byte aligned rows.
+        bool mf = false;
+        if constexpr (MT != LKV_F32) mf = a.q_dtype == MT && ((uintptr_t)a.q & 15u) == 0;
+        if (mf) {
+          if constexpr (MT != LKV_F32)
+            hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false, true>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
+        } else {
+          hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
+        }
         launched = true;
       } else if (a.loc != nullptr) {
         // hybrid: the 4-wave general instance below
