@@ -284,18 +284,63 @@ __device__ __forceinline__ float groups4_min(float x) {
   return x;
 }
 
+// The values of lanes l and l ^ M (M = 8, 16 or 32) without LDS traffic: DPP row_ror:8 within a
+// 16-lane row for M = 8; for M = 16 and 32, gfx950's v_permlane16_swap / v_permlane32_swap with
+// both operands x, which return the pair {x[l & ~M], x[l | M]}.
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8: lane i of a row reads lane (i + 8) % 16
+
+template <int M>
+__device__ __forceinline__ void lane_pair(float x, float& a, float& b) {
+  static_assert(M == 8 || M == 16 || M == 32, "pairs lanes 8, 16 or 32 apart");
+  if constexpr (M == 8) {
+    a = x;
+    b = dpp<kDppRowRor8>(x);
+  } else {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    uint32_t lo, hi;
+    if constexpr (M == 16) {
+      const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      lo = p[0];
+      hi = p[1];
+    } else {
+      const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      lo = p[0];
+      hi = p[1];
+    }
+    a = __builtin_bit_cast(float, lo);
+    b = __builtin_bit_cast(float, hi);
+  }
+}
+
+// x + x[l ^ M] and max(x, x[l ^ M]); addition and max are commutative, so every lane of the pair
+// gets the same bits as with a cross-lane shuffle.
+template <int M>
+__device__ __forceinline__ float pair_sum(float x) {
+  float a, b;
+  lane_pair<M>(x, a, b);
+  return a + b;
+}
+template <int M>
+__device__ __forceinline__ float pair_max(float x) {
+  float a, b;
+  lane_pair<M>(x, a, b);
+  return fmaxf(a, b);
+}
+
 // Combine the RG row groups of a wave (rows of 64 / RG lanes: lanes l, l ^ (64/RG), ...).
 template <int RG>
 __device__ __forceinline__ float groups_sum(float x) {
-#pragma unroll
-  for (int m = 64 / RG; m < 64; m <<= 1) x += xor_lane(x, m);
-  return x;
+  static_assert(RG == 4 || RG == 8, "rows of 16 or 8 lanes");
+  if constexpr (RG == 8) x = pair_sum<8>(x);
+  x = pair_sum<16>(x);
+  return pair_sum<32>(x);
 }
 template <int RG>
 __device__ __forceinline__ float groups_max(float x) {
-#pragma unroll
-  for (int m = 64 / RG; m < 64; m <<= 1) x = fmaxf(x, xor_lane(x, m));
-  return x;
+  static_assert(RG == 4 || RG == 8, "rows of 16 or 8 lanes");
+  if constexpr (RG == 8) x = pair_max<8>(x);
+  x = pair_max<16>(x);
+  return pair_max<32>(x);
 }
 
 }  // namespace lkv

@@ -519,8 +519,7 @@ __device__ __forceinline__ void consume_mf(const typename Mfma<MT>::V8 (&qb)[D /
       vld[u][i] = t0 + 4 * lg + i < lim[u];
       cm = vld[u][i] ? fmaxf(cm, sc[u][i]) : cm;
     }
-  cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
-  cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+  cm = lkv::pair_max<32>(lkv::pair_max<16>(cm));
   const float m_old = st.mh;
   const float m_new = fmaxf(m_old, cm);
   const bool live = m_new != -INFINITY;  // false while nothing valid has been seen
@@ -534,8 +533,7 @@ __device__ __forceinline__ void consume_mf(const typename Mfma<MT>::V8 (&qb)[D /
       p[u][i] = (vld[u][i] && live) ? exp2f(sc[u][i] - m_new) : 0.0f;
       ps += p[u][i];
     }
-  ps += __shfl_xor(ps, 16, 64);
-  ps += __shfl_xor(ps, 32, 64);
+  ps = lkv::pair_sum<32>(lkv::pair_sum<16>(ps));
   st.mh = live ? m_new : m_old;
   if (j < G) {
 #pragma unroll
