@@ -327,6 +327,76 @@ __device__ __forceinline__ float pair_max(float x) {
   return fmaxf(a, b);
 }
 
+// ---- whole-wave integer scans and reductions without LDS traffic ------------------------------
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {  // rows outside ROWS read 0
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROWS, 0xF, false);
+}
+template <int M>
+__device__ __forceinline__ void lane_pair_u32(uint32_t x, uint32_t& a, uint32_t& b) {
+  static_assert(M == 16 || M == 32, "pairs lanes 16 or 32 apart");
+  if constexpr (M == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    a = p[0];
+    b = p[1];
+  } else {
+    const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    a = p[0];
+    b = p[1];
+  }
+}
+
+// Inclusive prefix sum over the 64 lanes (ascending lane id): row_shr 1, 2, 4, 8 within each
+// 16-lane row, then row_bcast:15 adds row 0's total to row 1 and row 2's to row 3, and
+// row_bcast:31 adds the total of rows 0-1 to rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
+  x += dpp_u32<0x111>(x);
+  x += dpp_u32<0x112>(x);
+  x += dpp_u32<0x114>(x);
+  x += dpp_u32<0x118>(x);
+  x += dpp_u32<0x142, 0xA>(x);
+  x += dpp_u32<0x143, 0xC>(x);
+  return x;
+}
+
+// Minimum / maximum over the 64 lanes, in every lane.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  x = min(x, dpp_u32<kDppQuadSwap1>(x));
+  x = min(x, dpp_u32<kDppQuadSwap2>(x));
+  x = min(x, dpp_u32<kDppHalfMirror>(x));
+  x = min(x, dpp_u32<kDppMirror>(x));
+  uint32_t a, b;
+  lane_pair_u32<16>(x, a, b);
+  x = min(a, b);
+  lane_pair_u32<32>(x, a, b);
+  return min(a, b);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, dpp_u32<kDppQuadSwap1>(x));
+  x = max(x, dpp_u32<kDppQuadSwap2>(x));
+  x = max(x, dpp_u32<kDppHalfMirror>(x));
+  x = max(x, dpp_u32<kDppMirror>(x));
+  uint32_t a, b;
+  lane_pair_u32<16>(x, a, b);
+  x = max(a, b);
+  lane_pair_u32<32>(x, a, b);
+  return max(a, b);
+}
+
+// Sum / maximum over the 64 lanes of a wave, in every lane: DPP within each 16-lane row, then
+// the lane swaps across rows.
+__device__ __forceinline__ float wave_sum_f32(float x) {
+  x = row_sum<16>(x);
+  return pair_sum<32>(pair_sum<16>(x));
+}
+__device__ __forceinline__ float wave_max_f32(float x) {
+  x = fmaxf(x, dpp<kDppQuadSwap1>(x));
+  x = fmaxf(x, dpp<kDppQuadSwap2>(x));
+  x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppMirror>(x));
+  return pair_max<32>(pair_max<16>(x));
+}
+
 // Combine the RG row groups of a wave (rows of 64 / RG lanes: lanes l, l ^ (64/RG), ...).
 template <int RG>
 __device__ __forceinline__ float groups_sum(float x) {

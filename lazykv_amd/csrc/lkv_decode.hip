@@ -908,9 +908,7 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restri
   }
   const float m_t = t < S ? ml[(t * G + j) * 2] : -INFINITY;
   const float l_t = t < S ? ml[(t * G + j) * 2 + 1] : 0.0f;
-  float M = m_t;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  float M = lkv::wave_max_f32(m_t);
   if ((t & 63) == 0) s_red[t >> 6] = M;
   __syncthreads();
   M = s_red[0];
@@ -920,9 +918,7 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restri
   const bool any = M != -INFINITY;
   const float w_t = (t < S && any) ? exp2f(m_t - M) : 0.0f;
   if (t < S) s_w[t] = w_t;
-  float L = l_t * w_t;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+  float L = lkv::wave_sum_f32(l_t * w_t);
   if ((t & 63) == 0) s_red[t >> 6] = L;
   __syncthreads();
   L = 0.0f;
@@ -1102,12 +1098,7 @@ constexpr int kResPer = kMaxSlots / kResThreads;  // items and slots per thread
 
 __device__ __forceinline__ uint32_t res_block_scan(uint32_t v, uint32_t* slots, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    uint32_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const uint32_t x = lkv::wave_inclusive_sum(v);
   if (lane == 63) slots[wave] = x;
   __syncthreads();
   uint32_t before = 0, all = 0;

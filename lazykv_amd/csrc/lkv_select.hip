@@ -133,12 +133,7 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
 // per wave and is read after a barrier; the caller separates reuses of `slots` by a barrier.
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* slots, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    uint32_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const uint32_t x = lkv::wave_inclusive_sum(v);
   if (lane == 63) slots[wave] = x;
   __syncthreads();
   uint32_t before = 0, all = 0;
@@ -209,11 +204,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
     lmax = max(lmax, u < nlive ? key[u] : 0u);
   }
   // Workgroup min and max in one reduction.
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    lmin = min(lmin, (uint32_t)__shfl_xor(lmin, o, 64));
-    lmax = max(lmax, (uint32_t)__shfl_xor(lmax, o, 64));
-  }
+  lmin = lkv::wave_min_u32(lmin);
+  lmax = lkv::wave_max_u32(lmax);
   if (lane == 0) {
     mm[2 * wave] = lmin;
     mm[2 * wave + 1] = lmax;
@@ -432,11 +424,8 @@ __global__ __launch_bounds__(kSelThreads) void select_stream_kernel(const float*
     lmin = min(lmin, key);
     lmax = max(lmax, key);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    lmin = min(lmin, (uint32_t)__shfl_xor(lmin, o, 64));
-    lmax = max(lmax, (uint32_t)__shfl_xor(lmax, o, 64));
-  }
+  lmin = lkv::wave_min_u32(lmin);
+  lmax = lkv::wave_max_u32(lmax);
   if (lane == 0) {
     mm[2 * wave] = lmin;
     mm[2 * wave + 1] = lmax;
