@@ -292,6 +292,39 @@ def test_sparse_decode_matches_the_oracle(where: str, h: int, g: int, n: int, d:
     assert torch.equal(out_bf, out.to(torch.bfloat16)) and torch.equal(lse_bf, lse)
 
 
+@pytest.mark.parametrize(("d", "g", "dt"), [(128, 4, torch.bfloat16), (64, 4, torch.float16), (64, 2, torch.bfloat16), (128, 1, torch.float16)])
+def test_matrix_core_and_vector_scoring_agree(d: int, g: int, dt: torch.dtype) -> None:
+    """HBM launches score on the matrix cores when the query has the pool's dtype and 16-byte
+    aligned rows, and on the vector ALUs otherwise (a float32 query, or rows 2 bytes off): all three
+    match the oracle, and each other to float32 summation-order differences."""
+    from lazykv_amd import kernels
+
+    h, n, k, bs, fill = 8, 200, 40, 16, 11
+    w, pool = _pool_case(d + g, h, g, n, bs, d, dt)
+    store = pool.cuda()
+    gen = torch.Generator().manual_seed(d * g)
+    chosen = torch.stack([torch.randperm(n - 2, generator=gen)[:k] + 1 for _ in range(h)]).to(torch.int32)
+    src = kernels.pool_source(store)
+    q = w.query.to(dt)
+    flat = torch.empty(q.numel() + 1, dtype=dt, device="cuda")
+    q_off = flat[1:].view(q.shape)  # rows 2 bytes past a 16-byte boundary
+    q_off.copy_(q.cuda())
+    assert q_off.data_ptr() % 16 != 0
+    runs = {}
+    for name, qq in (("mfma", q.cuda()), ("unaligned", q_off), ("float32", q.float().cuda())):
+        runs[name] = kernels.sparse_decode(qq, n_kv=h, block_size=bs, scale=d**-0.5, sel=src, idx=chosen.cuda(), sink=src, sink_block=0, cur=src,
+                                           cur_block=n - 1, fill=fill, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    want_o, want_l = _oracle_decode(q, _f64(pool), chosen.numpy(), 0, n - 1, fill, d**-0.5, bs)
+    for name, (out, lse) in runs.items():
+        assert np.abs(out.cpu().numpy() - want_o).max() < TOL, name
+        assert np.abs(lse.cpu().numpy() - want_l).max() < TOL, name
+    o_m, l_m = runs["mfma"]
+    for name in ("unaligned", "float32"):
+        o_v, l_v = runs[name]
+        assert (o_m - o_v).abs().max().item() < 1e-5 and (l_m - l_v).abs().max().item() < 1e-5, name
+
+
 @pytest.mark.parametrize("where", ["hbm", "host"])
 @pytest.mark.parametrize("src_kind", ["f16", "bf16", "f32", "int8/f16", "int8/bf16"])
 @pytest.mark.parametrize(("bs", "d", "fill"), [(4, 64, 1), (8, 128, 8), (20, 64, 3), (20, 128, 17), (32, 64, 32), (64, 128, 50)])
