@@ -163,7 +163,12 @@ def test_layer_major_prefill_32k_1b_shape_writes_quant_py_records() -> None:
     out = None
     for s in range(0, n, chunk):
         out = model(input_ids=ids[:, s : s + chunk], past_key_values=full, use_cache=True, logits_to_keep=1)
-    assert torch.equal(got.last_logits, out.logits[0, -1].float())
+    # Both sides project the same last row onto the 128,256-entry vocabulary. The BLAS library does
+    # not promise run-to-run identical bits for that single-row product: after a long test session
+    # the two results once differed by one float16 step. So the logits are compared within four
+    # float16 steps of the largest; the tier's records below are compared bit for bit.
+    want_logits = out.logits[0, -1].float()
+    assert (got.last_logits - want_logits).abs().max().item() <= 4 * 2.0**-10 * max(1.0, want_logits.abs().max().item())
     assert not any(layer.is_initialized for layer in got.full.layers)
     nb = n // bs
     rng = np.random.default_rng(5)
