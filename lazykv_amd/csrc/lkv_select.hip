@@ -192,8 +192,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) key[u] = (u < npt && i0 + u < n) ? orderable(bound_h[i0 + u]) : 0u;
   }
-  // While the loads are in flight: clear the bitmap (read only after two later barriers).
+  // While the loads are in flight: clear the bitmap (read only after two later barriers) and the
+  // first pass's histogram (published by the min/max barrier below).
   for (int i = threadIdx.x; i < (kMaxCand + 31) / 32; i += kSelThreads) taken[i] = 0u;
+  for (int i = threadIdx.x; i < kBins; i += kSelThreads) hist[i] = 0u;
   // Slots u < nlive hold candidates (a count, not a per-slot flag array: an array of divergent
   // booleans lives in scalar register pairs and spills).
   const int nlive = max(0, min(npt, n - i0));
@@ -222,6 +224,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
   int need = k;  // keys still to take from [lo, hi]; every key above hi is taken
   uint32_t T;    // after the loop: take every key > T, `need` keys == T, and the marked keys
   uint32_t marked = 0u;  // bit u: key[u] lies in the final bin and ranks among the `need` best
+  bool first_pass = true;
 #pragma unroll 1
   while (true) {
     if (lo >= hi) {
@@ -232,8 +235,11 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
     const int bits = 32 - __clz(width);  // width < 2^bits
     const int shift = bits > 11 ? bits - 11 : 0;
     const int nb = (int)(width >> shift) + 1;  // at most 2048 bins
-    for (int i = threadIdx.x; i < nb; i += kSelThreads) hist[i] = 0;
-    __syncthreads();
+    if (!first_pass) {
+      for (int i = threadIdx.x; i < nb; i += kSelThreads) hist[i] = 0;
+      __syncthreads();
+    }
+    first_pass = false;
     // Branch-free: a key outside the range (or an empty slot) counts in this lane's spare bin.
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
@@ -338,20 +344,15 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
   const uint32_t tk = above_m | ties_taken;  // the slots this thread contributes, in index order
   int32_t* out_h = out_idx + (int64_t)h * idx_stride;
   if (!sorted) {
-    // The ids go to LDS at their output positions, then out in coalesced rounds of kStage.
-    for (int base = 0; base < k; base += kStage) {
-      const uint32_t lim = (uint32_t)min(base + kStage, k);
-      uint32_t pos = pos0;
+    // Each thread writes its ids straight to their output positions: a run of consecutive
+    // positions in index order, so the output is ascending (no staging round through LDS and its
+    // barrier).
+    uint32_t pos = pos0;
 #pragma unroll
-      for (int u = 0; u < kPerThread; ++u) {
-        const uint32_t bit = (tk >> u) & 1u;
-        const bool here = bit && pos >= (uint32_t)base && pos < lim;
-        stage[here ? pos - base : kStage + lane] = (uint32_t)(i0 + u);  // branch-free: spare slot otherwise
-        pos += bit;
-      }
-      __syncthreads();
-      for (int i = threadIdx.x; i < kStage && base + i < k; i += kSelThreads) out_h[base + i] = (int32_t)stage[i] + cand_offset;
-      __syncthreads();
+    for (int u = 0; u < kPerThread; ++u) {
+      const uint32_t bit = (tk >> u) & 1u;
+      if (bit && pos < (uint32_t)k) out_h[pos] = (int32_t)(i0 + u) + cand_offset;
+      pos += bit;
     }
     return;
   }
