@@ -400,10 +400,13 @@ def test_sparse_decode_reads_int8_records_in_place(dt: str) -> None:
     assert np.abs(lse.cpu().numpy() - want_l).max() < TOL
 
 
+@pytest.mark.parametrize("rem_where", ["host", "hbm"])
 @pytest.mark.parametrize("rem_kind", ["bf16", "int8"])
 @pytest.mark.parametrize("k", [5, 60, 118])
-def test_exact_split_reconstructs_full_attention(rem_kind: str, k: int) -> None:
-    """Selected from HBM + remainder from the host tier, merged in-kernel = attention over everything."""
+def test_exact_split_reconstructs_full_attention(rem_kind: str, k: int, rem_where: str) -> None:
+    """Selected from HBM + remainder from the host tier (or from HBM: the 8-wave kernels, whose
+    remainder runs skip the selected ids through a bitmap and take three blocks per softmax step),
+    merged in-kernel = attention over everything."""
     from lazykv_amd import kernels
     from lazykv_amd.pinned import pinned_empty
     from lazykv_amd.quant import packed_pair_bytes
@@ -412,13 +415,14 @@ def test_exact_split_reconstructs_full_attention(rem_kind: str, k: int) -> None:
     w, pool = _pool_case(k, h, g, n, bs, d, torch.bfloat16)
     dev_pool = pool.cuda()
     if rem_kind == "bf16":
-        host = pinned_empty(tuple(pool.shape), pool.dtype)
+        host = pinned_empty(tuple(pool.shape), pool.dtype) if rem_where == "host" else torch.empty(tuple(pool.shape), dtype=pool.dtype, device="cuda")
         host.copy_(pool)
         rem = kernels.pool_source(host)
         cold = _f64(pool)
     else:
         recs = R.pack(_bits(pool), "bf16")
-        host = pinned_empty((n, h, packed_pair_bytes(bs, d)), torch.uint8)
+        shape = (n, h, packed_pair_bytes(bs, d))
+        host = pinned_empty(shape, torch.uint8) if rem_where == "host" else torch.empty(shape, dtype=torch.uint8, device="cuda")
         host.copy_(torch.from_numpy(recs))
         rem = kernels.record_source(host, torch.bfloat16)
         cold = R.to_f32(R.unpack(recs.reshape(n * h, -1), bs, d, "bf16"), "bf16").reshape(n, h, 2, bs, d).astype(np.float64)
