@@ -17,7 +17,9 @@
 // (block, head) pair at a time with all G query heads of the group, so every KV byte is read
 // once. A row's channels are spread over 16 lanes at d 128 and 8 lanes at d 64, 8 channels each
 // (Lanes<D>), so a wave-wide load of 16-byte lane segments covers 4 or 8 rows. Scores are DPP
-// sums over a row's lanes; the online softmax runs in base 2 with the scale folded into q.
+// sums over a row's lanes; the online softmax runs in base 2 with the scale folded into q. The
+// 8-wave model-dtype instances score on the matrix cores instead (MF, below), up to three pairs
+// per softmax step.
 //
 // Merge. Waves combine in LDS, workgroups write (m, l, o) partials to the workspace, and a second
 // launch folds each query head's partials into out and lse. (A last-arriver merge inside one
@@ -356,9 +358,10 @@ __device__ __forceinline__ void consume_chunk(const float (&q)[G][Lanes<D>::EPL]
   }
 }
 
-// Pairs a wave keeps in flight in the remainder segment: one (measured on runs of consecutive
-// blocks from HBM and from host memory, two were no faster). The selected segment takes two in
-// kernels without int8 code (see the kernel), one otherwise.
+// Pairs a wave keeps in flight in the remainder segment of the vector-path instances: one
+// (measured on runs of consecutive blocks from HBM and from host memory, two were no faster). The
+// selected segment takes two in the 8-wave int8 instances, one in the 4-wave general instance; the
+// matrix-core instances take up to three in both segments.
 template <int G>
 constexpr int kPairs = 1;
 
@@ -759,10 +762,10 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       const int je = min(last, has_sink + n_sel) - has_sink;
       const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
       // The hybrid branch is compiled only into the 4-wave general instance, which every hybrid
-      // launch takes. The other instances keep two selected pairs in flight per wave: with about two
-      // items per wave in the HBM plan, both loads are issued before either is consumed (int8
-      // records in HBM 24.4 -> 23.5 us, identical results). Float32 pools keep one (two would
-      // spill).
+      // launch takes. The 8-wave vector-path instances keep two selected pairs in flight per wave:
+      // with about two items per wave in the HBM plan, both loads are issued before either is
+      // consumed (int8 records in HBM 24.4 -> 23.5 us, identical results). Float32 pools keep one
+      // (two would spill).
       constexpr bool HYB = I8 && NT == kThreads;
       constexpr int NPA = (HYB || MT == LKV_F32) ? 1 : 2;
       for (int j = js + wave; j < je; j += NPA * NW) {
