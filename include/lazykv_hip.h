@@ -78,7 +78,7 @@ typedef struct lkv_decode_desc {
   int32_t n_q;       /* query heads */
   int32_t n_kv;      /* KV heads; n_q % n_kv == 0 (GQA) */
   int32_t head_dim;  /* 64 or 128 */
-  int32_t block_size;/* tokens per block; a multiple of 4, at most 64 */
+  int32_t block_size;/* tokens per block; a multiple of 4, at most 256 */
   float scale;       /* softmax scaling (Llama: head_dim ** -0.5) */
   int32_t k;         /* entries per KV head in `idx` */
   int32_t attend_selected; /* 1: attend the idx blocks from `sel`; 0: idx only excludes */

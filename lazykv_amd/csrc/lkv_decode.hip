@@ -1263,8 +1263,8 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
   LKV_CHECK_ARG(d.n_kv > 0 && d.n_q > 0 && d.n_q % d.n_kv == 0, "n_q=%d must be a positive multiple of n_kv=%d",
                 d.n_q, d.n_kv);
   LKV_CHECK_ARG(d.head_dim == 64 || d.head_dim == 128, "head_dim %d unsupported (64 or 128)", d.head_dim);
-  LKV_CHECK_ARG(d.block_size >= 4 && d.block_size <= 64 && d.block_size % 4 == 0,
-                "block_size %d unsupported (a multiple of 4 up to 64)", d.block_size);
+  LKV_CHECK_ARG(d.block_size >= 4 && d.block_size <= 256 && d.block_size % 4 == 0,
+                "block_size %d unsupported (a multiple of 4 up to 256)", d.block_size);
   LKV_CHECK_ARG(d.k >= 0, "negative k");
   LKV_CHECK_ARG(lkv_is_model_dtype(q_dtype) && lkv_is_model_dtype(out_dtype), "bad q/out dtype");
   LKV_CHECK_ARG(d.rem_last >= d.rem_first && d.rem_first >= 0, "bad remainder range");

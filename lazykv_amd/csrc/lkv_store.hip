@@ -335,8 +335,8 @@ extern "C" int lkv_store_blocks(uintptr_t stream, const lkv_kv_source* src, cons
   LKV_CHECK_ARG(src != nullptr && src->k != nullptr, "source missing");
   LKV_CHECK_ARG(n_kv > 0 && n_blocks >= 0 && first_block >= 0, "bad block range");
   LKV_CHECK_ARG(head_dim == 64 || head_dim == 128, "head_dim %d unsupported (64 or 128)", head_dim);
-  LKV_CHECK_ARG(block_size >= 4 && block_size <= 64 && block_size % 4 == 0,
-                "block_size %d unsupported (a multiple of 4 up to 64)", block_size);
+  LKV_CHECK_ARG(block_size >= 4 && block_size <= 256 && block_size % 4 == 0,
+                "block_size %d unsupported (a multiple of 4 up to 256)", block_size);
   LKV_CHECK_ARG((kmin == nullptr) == (kmax == nullptr), "kmin and kmax go together");
   LKV_CHECK_ARG((int64_t)first_block + n_blocks <= src->n_blocks, "blocks %d..%d outside the source (%lld blocks)",
                 first_block, first_block + n_blocks, (long long)src->n_blocks);
@@ -421,8 +421,8 @@ extern "C" int lkv_unpack_int8(uintptr_t stream, const void* records, int64_t m,
   LKV_CHECK_ARG(pairs != nullptr && records != nullptr, "NULL pointer");
   LKV_CHECK_ARG(m >= 0, "bad record count");
   LKV_CHECK_ARG(head_dim == 64 || head_dim == 128, "head_dim %d unsupported (64 or 128)", head_dim);
-  LKV_CHECK_ARG(block_size >= 4 && block_size <= 64 && block_size % 4 == 0,
-                "block_size %d unsupported (a multiple of 4 up to 64)", block_size);
+  LKV_CHECK_ARG(block_size >= 4 && block_size <= 256 && block_size % 4 == 0,
+                "block_size %d unsupported (a multiple of 4 up to 256)", block_size);
   LKV_CHECK_ARG(lkv_is_model_dtype(dtype), "bad dtype");
   if (m == 0) return LKV_OK;
   hipStream_t s = (hipStream_t)stream;

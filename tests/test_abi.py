@@ -75,6 +75,9 @@ def test_bad_arguments_are_rejected_before_any_launch(lib) -> None:  # noqa: ANN
     desc = _lib.DecodeDesc(32, 8, 128, 17, 0.088, 0, 1, 0, -1, 1, 0, 0)
     rc = lib.lkv_sparse_decode(0, ctypes.byref(desc), dummy, _lib.BF16, None, None, 0, None, None, None, dummy, _lib.BF16, dummy, dummy, 1 << 20)
     assert rc == _lib.LKV_ERR_INVALID and b"block_size" in lib.lkv_last_error()
+    desc = _lib.DecodeDesc(32, 8, 128, 260, 0.088, 0, 1, 0, -1, 1, 0, 0)  # past the largest block size (256)
+    rc = lib.lkv_sparse_decode(0, ctypes.byref(desc), dummy, _lib.BF16, None, None, 0, None, None, None, dummy, _lib.BF16, dummy, dummy, 1 << 20)
+    assert rc == _lib.LKV_ERR_INVALID and b"block_size" in lib.lkv_last_error()
 
 
 def test_errors_map_to_the_reference_exception_types() -> None:

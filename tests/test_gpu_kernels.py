@@ -61,7 +61,7 @@ def test_pack_and_unpack_reproduce_the_reference_bytes(key: str, dt: str, bs: in
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-@pytest.mark.parametrize(("bs", "d"), [(16, 128), (16, 64), (8, 64), (64, 128)])
+@pytest.mark.parametrize(("bs", "d"), [(16, 128), (16, 64), (8, 64), (64, 128), (128, 64), (256, 128)])
 def test_pack_unpack_bit_exact_on_seeded_data(dt: str, bs: int, d: int) -> None:
     from lazykv_amd import quant
 
@@ -327,9 +327,9 @@ def test_matrix_core_and_vector_scoring_agree(d: int, g: int, dt: torch.dtype) -
 
 @pytest.mark.parametrize("where", ["hbm", "host"])
 @pytest.mark.parametrize("src_kind", ["f16", "bf16", "f32", "int8/f16", "int8/bf16"])
-@pytest.mark.parametrize(("bs", "d", "fill"), [(4, 64, 1), (8, 128, 8), (20, 64, 3), (20, 128, 17), (32, 64, 32), (64, 128, 50)])
+@pytest.mark.parametrize(("bs", "d", "fill"), [(4, 64, 1), (8, 128, 8), (20, 64, 3), (20, 128, 17), (32, 64, 32), (64, 128, 50), (128, 64, 100), (256, 128, 255)])
 def test_sparse_decode_block_sizes_and_dtypes(where: str, src_kind: str, bs: int, d: int, fill: int) -> None:
-    """Every block size the kernels take (multiples of 4 up to 64, including chunks shorter than
+    """Every block size the kernels take (multiples of 4 up to 256, including chunks shorter than
     16 rows and a 4-row tail chunk at bs 20), partial and full current blocks, each model dtype and
     int8 records (read in place, dequantised in the load), from HBM and from host memory."""
     from lazykv_amd import kernels

@@ -39,7 +39,8 @@ class _Shadow:
     current block are always exact (lazykv/tiered.py:200-205).
     """
 
-    def __init__(self, keys: torch.Tensor, values: torch.Tensor, quant: str | None) -> None:
+    def __init__(self, keys: torch.Tensor, values: torch.Tensor, quant: str | None, bs: int = BS) -> None:
+        self.bs = bs
         self.k = list(_f64(keys[0]).transpose(1, 0, 2))  # per token [h, d]
         self.v = list(_f64(values[0]).transpose(1, 0, 2))
         self.kb = list(_bits(keys[0]).transpose(1, 0, 2))
@@ -54,13 +55,14 @@ class _Shadow:
 
     def block(self, b: int, sealed: bool) -> tuple[np.ndarray, np.ndarray]:
         """[h, bs, d] keys and values of block b as the tier stores it."""
-        k = np.stack(self.k[b * BS : (b + 1) * BS], axis=1)
-        v = np.stack(self.v[b * BS : (b + 1) * BS], axis=1)
+        bs = self.bs
+        k = np.stack(self.k[b * bs : (b + 1) * bs], axis=1)
+        v = np.stack(self.v[b * bs : (b + 1) * bs], axis=1)
         if self.quant == "int8" and sealed and b > 0:
-            kb = np.stack(self.kb[b * BS : (b + 1) * BS], axis=1)
-            vb = np.stack(self.vb[b * BS : (b + 1) * BS], axis=1)
+            kb = np.stack(self.kb[b * bs : (b + 1) * bs], axis=1)
+            vb = np.stack(self.vb[b * bs : (b + 1) * bs], axis=1)
             pairs = np.stack([kb, vb], axis=1)  # [h, 2, bs, d]
-            deq = R.to_f32(R.unpack(R.pack(pairs, "bf16"), BS, D, "bf16"), "bf16").reshape(H, 2, BS, D).astype(np.float64)
+            deq = R.to_f32(R.unpack(R.pack(pairs, "bf16"), bs, D, "bf16"), "bf16").reshape(H, 2, bs, D).astype(np.float64)
             return deq[:, 0], deq[:, 1]
         return k, v
 
@@ -70,6 +72,7 @@ class _Shadow:
 
 
 def _check_step(layer, shadow: _Shadow, q: torch.Tensor, exact_store: bool = False) -> None:
+    BS = shadow.bs  # noqa: N806 -- the layer's block size
     n_sealed, fill = layer.candidates()
     idx = layer.rank(q.view(1, -1, 1, D))
     out32 = torch.empty((H * G, D), dtype=torch.float32, device="cuda")
@@ -139,6 +142,25 @@ def test_decode_through_seals_matches_the_oracle(fetch: str, quant: str | None) 
         if step % 4 == 3 or step in (0, 8, 9):
             _check_step(layer, shadow, q.cuda())
     assert layer.candidates() == (64, 16)  # 1040 tokens, sealed lazily when tokens 1009 and 1025 arrived
+
+
+@pytest.mark.parametrize(("bs", "fetch", "quant"), [(128, "zerocopy", None), (128, "hybrid", "int8"), (256, "resident", None), (256, "zerocopy", "int8")])
+def test_decode_through_seals_at_large_block_sizes(bs: int, fetch: str, quant: str | None) -> None:
+    """Blocks of 128 and 256 tokens (the reference sweeps 16-256): the prompt ends 3 tokens short
+    of a block, so the appends seal it; every step is checked against the oracle."""
+    from lazykv_amd.tiered import TieredLayer
+
+    keys, values, gen = _prompt(20 + bs, 6 * bs - 3)
+    layer = TieredLayer(keys.cuda(), values.cuda(), 2, bs, 12 * bs, quant=quant, fetch=fetch)
+    shadow = _Shadow(keys, values, quant, bs)
+    for step in range(8):
+        k = torch.randn((1, H, 1, D), generator=gen).to(torch.bfloat16)
+        v = torch.randn((1, H, 1, D), generator=gen).to(torch.bfloat16)
+        layer.append(k.cuda(), v.cuda())
+        shadow.append(k, v)
+        q = torch.randn((H * G, D), generator=gen).to(torch.bfloat16)
+        _check_step(layer, shadow, q.cuda())
+    assert layer.candidates() == (6, 5)  # 6 bs + 5 tokens: the sixth block sealed when token 6 bs + 1 arrived
 
 
 @pytest.mark.parametrize("quant", [None, "int8"])
