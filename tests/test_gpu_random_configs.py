@@ -1,0 +1,115 @@
+"""Seeded random decode configurations against the float64 oracle (GPU).
+
+Each case draws the number of KV heads, the group size, head_dim, block size, budget, current-block
+fill, model dtype, where the selected blocks live (HBM or mapped host memory), whether they are
+int8 records, and whether an exact remainder partial is added (from HBM or host memory, model
+dtype or int8). The kernels then take every launch shape and instance in combinations the
+hand-picked cases do not: 4- and 8-wave workgroups, the matrix-core and vector instances, one to
+three pairs per step, chunked and short blocks. Bars as elsewhere: float32 output and LSE within
+2e-3 of the float64 oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+N_CASES = 64
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _case(seed: int) -> dict:
+    rng = np.random.default_rng(1000 + seed)
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([4, 8, 16, 16, 16, 20, 32, 64, 128, 256]))
+    n = int(rng.integers(8, max(9, 4096 // bs)))
+    return {
+        "h": int(rng.choice([1, 2, 3, 4, 8])),
+        "g": int(rng.choice([1, 2, 4, 4, 8])),
+        "d": d,
+        "bs": bs,
+        "n": n,
+        "k": int(rng.integers(1, n - 1)),
+        "fill": int(rng.integers(1, bs + 1)),
+        "dt": [torch.float16, torch.bfloat16][int(rng.integers(0, 2))],
+        "sel_where": str(rng.choice(["hbm", "hbm", "host"])),
+        "sel_int8": bool(rng.random() < 0.3),
+        "rem": str(rng.choice(["none", "none", "hbm", "host"])),
+        "rem_int8": bool(rng.random() < 0.5),
+    }
+
+
+def _place(t: torch.Tensor, where: str) -> torch.Tensor:
+    from lazykv_amd.pinned import pinned_empty
+
+    out = pinned_empty(tuple(t.shape), t.dtype) if where == "host" else torch.empty(tuple(t.shape), dtype=t.dtype, device="cuda")
+    out.copy_(t)
+    return out
+
+
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_random_decode_configuration_matches_the_oracle(seed: int) -> None:
+    from lazykv_amd import kernels
+    from lazykv_amd.quant import packed_pair_bytes
+    from lazykv_amd.workload import draw_layer, to_pool
+
+    c = _case(seed)
+    h, g, d, bs, n, k, fill, dt = c["h"], c["g"], c["d"], c["bs"], c["n"], c["k"], c["fill"], c["dt"]
+    name = "bf16" if dt == torch.bfloat16 else "f16"
+    print(f"case {seed}: {c}", flush=True)
+    w = draw_layer(seed, h * g, h, d, n * bs, bs, dt)
+    pool = to_pool(w.keys, w.values, bs)  # [n, h, 2, bs, d]
+    exact = pool.double().numpy()
+    recs = R.pack(_bits(pool), name)  # [n, h, P]
+    deq = R.to_f32(R.unpack(recs.reshape(n * h, -1), bs, d, name), name).reshape(n, h, 2, bs, d).astype(np.float64)
+
+    def source(int8: bool, where: str):  # noqa: ANN202
+        if int8:
+            store = _place(torch.from_numpy(recs).view(torch.uint8).reshape(n, h, packed_pair_bytes(bs, d)), where)
+            return kernels.record_source(store, dt), deq, store
+        store = _place(pool, where)
+        return kernels.pool_source(store), exact, store
+
+    sel, sel_vals, keep_sel = source(c["sel_int8"], c["sel_where"])
+    slots = pool[[0, n - 1]].contiguous().cuda()  # sink and current in the model dtype, in HBM
+    ss = kernels.pool_source(slots)
+    gen = torch.Generator().manual_seed(seed)
+    chosen = torch.stack([torch.randperm(n - 2, generator=gen)[:k] + 1 for _ in range(h)]).to(torch.int32)
+    extra: dict = {}
+    rem_vals = None
+    keep_rem = None
+    if c["rem"] != "none":
+        rem, rem_vals, keep_rem = source(c["rem_int8"], c["rem"])
+        extra = {"rem": rem, "rem_range": (1, n - 1)}
+    out, lse = kernels.sparse_decode(w.query.cuda(), n_kv=h, block_size=bs, scale=d**-0.5, sel=sel, idx=chosen.cuda(), sink=ss, sink_block=0, cur=ss,
+                                     cur_block=1, fill=fill, out_dtype=torch.float32, **extra)
+    torch.cuda.synchronize()
+    del keep_sel, keep_rem
+    q = w.query.double().numpy()
+    ks, vs = [], []
+    for j in range(h):
+        picked = set(chosen[j].tolist())
+        kk, vv = [exact[0, j, 0]], [exact[0, j, 1]]
+        for b in range(1, n - 1):
+            if b in picked:
+                kk.append(sel_vals[b, j, 0])
+                vv.append(sel_vals[b, j, 1])
+            elif rem_vals is not None:
+                kk.append(rem_vals[b, j, 0])
+                vv.append(rem_vals[b, j, 1])
+        kk.append(exact[n - 1, j, 0, :fill])
+        vv.append(exact[n - 1, j, 1, :fill])
+        ks.append(np.concatenate(kk))
+        vs.append(np.concatenate(vv))
+    want_o, want_l = R.attend_tokens(q, ks, vs, d**-0.5)
+    assert np.abs(out.cpu().numpy() - want_o).max() < TOL, c
+    assert np.abs(lse.cpu().numpy() - want_l).max() < TOL, c
