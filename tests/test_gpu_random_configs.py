@@ -6,7 +6,9 @@ int8 records, and whether an exact remainder partial is added (from HBM or host 
 dtype or int8). The kernels then take every launch shape and instance in combinations the
 hand-picked cases do not: 4- and 8-wave workgroups, the matrix-core and vector instances, one to
 three pairs per step, chunked and short blocks. Bars as elsewhere: float32 output and LSE within
-2e-3 of the float64 oracle.
+2e-3 of the float64 oracle. A second sweep draws bound + top-K calls (candidate counts on both
+sides of the in-register limit, offsets, sorted and ascending output): the float32 bounds within
+the accumulation error bound of the float64 ones, the selected sets under the near-tie rule.
 """
 
 from __future__ import annotations
@@ -113,3 +115,58 @@ def test_random_decode_configuration_matches_the_oracle(seed: int) -> None:
     want_o, want_l = R.attend_tokens(q, ks, vs, d**-0.5)
     assert np.abs(out.cpu().numpy() - want_o).max() < TOL, c
     assert np.abs(lse.cpu().numpy() - want_l).max() < TOL, c
+
+
+def _sel_case(seed: int) -> dict:
+    rng = np.random.default_rng(5000 + seed)
+    n = int(rng.choice([5, 64, 500, 2046, 4094, 8190, 12288, 12289, 20000]))
+    h = int(rng.choice([1, 2, 3, 4, 8]))
+    if h * n > 60000:
+        h = max(1, 60000 // n)
+    sorted_ = bool(rng.random() < 0.3)
+    return {
+        "d": int(rng.choice([64, 128])),
+        "h": h,
+        "g": int(rng.choice([1, 2, 4, 8])),
+        "n": n,
+        "offset": int(rng.integers(0, 3)),
+        "k": int(rng.integers(1, min(n, 2048 if sorted_ else 4096) + 1)),
+        "sorted": sorted_,
+        "dt": [torch.float16, torch.bfloat16][int(rng.integers(0, 2))],
+    }
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_selection_matches_the_oracle(seed: int) -> None:
+    """Bound + top-K over random metadata: up to 20,000 candidates per head (past the 12,288 that
+    one workgroup holds in registers), offsets, unsorted (ascending ids) and sorted (descending
+    bound, lower id first on ties) output."""
+    from lazykv_amd import kernels
+
+    c = _sel_case(seed)
+    d, h, g, n, off, k, dt = c["d"], c["h"], c["g"], c["n"], c["offset"], c["k"], c["dt"]
+    print(f"selection case {seed}: {c}", flush=True)
+    gen = torch.Generator().manual_seed(seed)
+    cap = off + n + 1
+    centre = torch.randn((1, h, cap, d), generator=gen) * (torch.rand((1, h, 1, d), generator=gen) * 1.5 + 0.5)
+    kmin = (centre - torch.rand((1, h, cap, d), generator=gen)).to(dt)
+    kmax = (centre + torch.rand((1, h, cap, d), generator=gen)).to(dt)
+    q = torch.randn((h * g, d), generator=gen).to(dt)
+    bounds = torch.empty((h, n), dtype=torch.float32, device="cuda")
+    idx = kernels.bound_topk(q.cuda(), kmin.cuda(), kmax.cuda(), k, cand_offset=off, n_cand=n, sorted_=c["sorted"], out_bound=bounds)
+    torch.cuda.synchronize()
+    qf = q.double().numpy()
+    lo, hi = kmin[0, :, off : off + n].double().numpy(), kmax[0, :, off : off + n].double().numpy()
+    want = R.quest_bound(qf, lo, hi)
+    err = float(np.abs(qf).max() * np.maximum(np.abs(lo), np.abs(hi)).sum(-1).max()) * 2.0**-19
+    got_b = bounds.cpu().numpy()
+    assert np.abs(got_b - want).max() <= err
+    top = idx.cpu().numpy() - off
+    for j in range(h):
+        ok, _ = R.selection_ok(top[j], want[j], k, abs_err=err)
+        assert ok, (j, c)
+        if c["sorted"]:
+            b = got_b[j][top[j]]
+            assert (np.diff(b) <= 0).all() and all(top[j][i] < top[j][i + 1] for i in range(k - 1) if b[i] == b[i + 1]), c
+        else:
+            assert (np.diff(top[j]) > 0).all(), c
