@@ -170,3 +170,66 @@ def test_random_selection_matches_the_oracle(seed: int) -> None:
             assert (np.diff(b) <= 0).all() and all(top[j][i] < top[j][i + 1] for i in range(k - 1) if b[i] == b[i + 1]), c
         else:
             assert (np.diff(top[j]) > 0).all(), c
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_block_store_matches_the_oracle(seed: int) -> None:
+    """store_blocks over random ranges: metadata only, a copy into the pool layout, or int8 records
+    (HBM or mapped host memory), bs 4-256. Copies and records bit for bit (quant.py's pack), the
+    metadata the exact min/max of the keys as stored (dequantised for records), and nothing outside
+    the range touched."""
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+    from lazykv_amd.quant import packed_pair_bytes
+
+    rng = np.random.default_rng(9000 + seed)
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([4, 8, 16, 16, 20, 32, 64, 128, 256]))
+    h = int(rng.integers(1, 9))
+    n = int(rng.integers(2, max(3, 2048 // bs)))
+    first = int(rng.integers(0, n))
+    count = int(rng.integers(1, n - first + 1))
+    dt = [torch.float16, torch.bfloat16][int(rng.integers(0, 2))]
+    mode = str(rng.choice(["meta", "copy", "int8"]))
+    where = str(rng.choice(["hbm", "host"]))
+    name = "bf16" if dt == torch.bfloat16 else "f16"
+    print(f"store case {seed}: d={d} bs={bs} h={h} n={n} first={first} count={count} {dt} {mode} {where}", flush=True)
+    gen = torch.Generator().manual_seed(seed)
+    keys = (torch.randn((1, h, n * bs, d), generator=gen) * (torch.rand((1, h, 1, d), generator=gen) * 3 + 0.1)).to(dt)
+    values = torch.randn((1, h, n * bs, d), generator=gen).to(dt)
+    pairs = torch.stack([keys[0], values[0]], dim=1).view(h, 2, n, bs, d).permute(2, 0, 1, 3, 4).contiguous()  # [n, h, 2, bs, d]
+    kmin = torch.zeros((1, h, n, d), dtype=dt, device="cuda")
+    kmax = torch.zeros_like(kmin)
+
+    def alloc(shape, dtype):  # noqa: ANN001, ANN202
+        t = pinned_empty(shape, dtype) if where == "host" else torch.empty(shape, dtype=dtype, device="cuda")
+        t.zero_()
+        return t
+
+    dst, store = None, None
+    if mode == "copy":
+        store = alloc((n, h, 2, bs, d), dt)
+        dst = kernels.pool_source(store)
+    elif mode == "int8":
+        store = alloc((n, h, packed_pair_bytes(bs, d)), torch.uint8)
+        dst = kernels.record_source(store, dt)
+    kernels.store_blocks(kernels.dense_source(keys.cuda(), values.cuda(), bs), dst=dst, n_kv=h, head_dim=d, block_size=bs, first_block=first, n_blocks=count,
+                         kmin=kmin, kmax=kmax)
+    torch.cuda.synchronize()
+    rng_b = slice(first, first + count)
+    if mode == "int8":
+        want = R.pack(_bits(pairs[rng_b]), name)
+        got = store.cpu().numpy()
+        assert np.array_equal(got[rng_b], want)
+        assert not got[:first].any() and not got[first + count :].any()
+        stored_keys = R.to_f32(R.unpack(want.reshape(count * h, -1), bs, d, name), name).reshape(count, h, 2, bs, d)[:, :, 0].astype(np.float64)
+    else:
+        if mode == "copy":
+            got = store.cpu()
+            assert torch.equal(got[rng_b], pairs[rng_b])
+            assert not got[:first].any() and not got[first + count :].any()
+        stored_keys = pairs[rng_b][:, :, 0].double().numpy()
+    mn = kmin[0].cpu().double().numpy().transpose(1, 0, 2)  # [n, h, d]
+    mx = kmax[0].cpu().double().numpy().transpose(1, 0, 2)
+    assert np.array_equal(mn[rng_b], stored_keys.min(axis=2)) and np.array_equal(mx[rng_b], stored_keys.max(axis=2))
+    assert not mn[:first].any() and not mn[first + count :].any()
