@@ -118,6 +118,62 @@ def test_questview_decodes_like_the_resident_tier() -> None:
     assert torch.equal(rows["quest"], rows["resident"])
 
 
+def test_zerocopy_and_hybrid_tiers_decode_like_questview() -> None:
+    """After lazykv/tests/test_tiered.py:190-217: the zero-copy tier reads the selected blocks of
+    the pinned pool in place (VRAM holds only the sink and the current block), over 40 decode
+    steps that cross two seals, and so does the hybrid tier through its HBM slots. Both make the
+    same number of selections as QuestView over the dense cache and give the same log-probabilities
+    within 2e-2; the zero-copy byte count is the selected pairs times the pair size. Bit identity
+    is not asked: a host source is cut into fewer, longer runs per workgroup than an HBM one, so
+    the partials are combined in another order."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from lazykv_amd.attention import IMPLEMENTATION_NAME, install
+    from lazykv_amd.cache import FullGPUCache
+    from lazykv_amd.selection import QuestView
+    from lazykv_amd.tiered import TieredCache
+
+    install()
+    torch.manual_seed(0)
+    cfg = LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=3, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+                      vocab_size=512, max_position_embeddings=4096)
+    with torch.device("cuda"):
+        model = LlamaForCausalLM(copy.deepcopy(cfg))
+    model.set_attn_implementation(IMPLEMENTATION_NAME)
+    model = model.to(dtype=torch.float16).eval()
+    ids = torch.randint(0, cfg.vocab_size, (1, 190), device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+    prompt = 150
+    full = FullGPUCache(cfg.num_hidden_layers, 512)
+    with torch.inference_mode():
+        first = model(input_ids=ids[:, :prompt], past_key_values=full, use_cache=True).logits[0, -1].float()
+    kv = [(layer.keys[:, :, :prompt].clone(), layer.values[:, :, :prompt].clone()) for layer in full.layers]
+    caches = {
+        "quest": QuestView(full, 3, BS, dense_layers=1, bound_dtype=torch.float32),
+        "zerocopy": TieredCache(FullGPUCache.from_kv(kv, 512), 3, BS, 512, dense_layers=1, fetch="zerocopy"),
+        "hybrid": TieredCache(FullGPUCache.from_kv(kv, 512), 3, BS, 512, dense_layers=1, fetch="hybrid"),
+    }
+    rows = {}
+    for name, cache in caches.items():
+        out = [torch.log_softmax(first, -1)]
+        with torch.inference_mode():
+            for t in range(prompt, 190):
+                logits = model(input_ids=ids[:, t : t + 1], past_key_values=cache, use_cache=True, **cache.model_kwargs()).logits[0, -1]
+                out.append(torch.log_softmax(logits.float(), -1))
+        rows[name] = torch.stack(out)
+    assert torch.isfinite(rows["quest"]).all()
+    for name in ("zerocopy", "hybrid"):
+        c = caches[name].counters
+        assert c.selections == caches["quest"].counters.selections == 2 * 40, name
+        assert c.seals == 2 * 2, name  # blocks 9 and 10 seal in both selecting layers
+        assert (rows[name] - rows["quest"]).abs().max().item() < 2e-2, name
+    zc = caches["zerocopy"]
+    c = zc.counters
+    pair = next(iter(zc.tiers.values())).pair_bytes
+    assert c.zerocopy_bytes == c.selected_pairs * pair > 0
+    for t in zc.tiers.values():
+        assert t.n_slots == 0 and t.pool.shape[0] == 2  # VRAM: the sink and the current block
+
+
 @pytest.mark.parametrize(("fetch", "quant"), [("zerocopy", None), ("zerocopy", "int8"), ("resident", None), ("hybrid", None)])
 def test_tier_stats_count_what_vram_does_not_hold(fetch: str, quant: str | None) -> None:
     from lazykv_amd.quant import packed_pair_bytes
