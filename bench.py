@@ -73,6 +73,8 @@ def main() -> int:
     p.add_argument("--layers", type=int, default=None)
     p.add_argument("--tokens", type=int, default=None)
     p.add_argument("--k", type=int, default=None, help="selected blocks per KV head (default: the workload's)")
+    p.add_argument("--block-size", type=int, default=16, choices=[16, 32, 64, 128, 256],
+                   help="tokens per block; without --k the workload's K is scaled to keep its token budget")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["zerocopy", "hbm"], default=None, help="decode128k: one leg only")
@@ -86,11 +88,15 @@ def main() -> int:
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path has no multi-GPU mode (asked for --gpus {args.gpus}).", file=sys.stderr)
         return 2
+    global BS
+    BS = args.block_size
     spec = dict(WORKLOADS[args.workload])
     spec["layers"] = args.layers or spec["layers"]
     spec["tokens"] = args.tokens or spec["tokens"]
     if args.k:
         spec["k"] = (args.k,)
+    elif BS != 16:
+        spec["k"] = tuple(max(1, k * 16 // BS) for k in spec["k"])
     runners = {"prefill": run_prefill, "hybrid": run_hybrid}
     out = runners.get(spec["kind"], run_decode)(args, spec)
     print(json.dumps(out), flush=True)
@@ -442,8 +448,8 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
     main_leg = next(iter(res))
     m = legs_out[main_leg]
     names = {
-        "host": f"Llama-3.1-8B-shaped tiered decode step: {L} selecting layers, {T} tokens, 16-token blocks, K={m['k']} of {n_cand} candidates per KV head (6.25% budget), bf16 KV in mapped pinned host memory",
-        "hbm": f"Llama-3.2-1B-shaped decode layer: {T} tokens, d {d}, float16, 16-token blocks, K={m['k']} of {n_cand} candidates per KV head, all in HBM ({L} rotated layer instances)",
+        "host": f"Llama-3.1-8B-shaped tiered decode step: {L} selecting layers, {T} tokens, {BS}-token blocks, K={m['k']} of {n_cand} candidates per KV head ({100 * m['k'] * BS / T:g}% budget), bf16 KV in mapped pinned host memory",
+        "hbm": f"Llama-3.2-1B-shaped decode layer: {T} tokens, d {d}, float16, {BS}-token blocks, K={m['k']} of {n_cand} candidates per KV head, all in HBM ({L} rotated layer instances)",
         "int8": f"Llama-3.2-1B-shaped decode step: {L} selecting layers, {T} tokens, d {d}, float16, K={m['k']} of {n_cand} per KV head, sealed blocks as int8 records in {'HBM' if args.tier_where == 'hbm' else 'mapped host memory'}, dequantised on load",
         "exact": f"Llama-3.1-8B-shaped exact tiered decode step: {L} layers, {T} tokens, bf16, K of {n_cand} from the exact HBM store, every other sealed block from the int8 host tier, merged by LSE",
     }

@@ -968,6 +968,8 @@ struct PlanHints {
   size_t sel_pair = 0, rem_pair = 0;
 };
 
+constexpr int kHostMinWgs = 64;  // floor on the workgroups of a launch that reads selected pairs from host memory
+
 // Host segments are split into fewer, longer runs than HBM ones: enough workgroups that one pair
 // per wave keeps the host read budget in flight, and no more -- lkv_host_read_inflight for the
 // scattered selected pairs, lkv_host_stream_inflight for the remainder's runs of consecutive
@@ -1018,7 +1020,14 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
     }
   }
   if (hint.sel_host && n_sel > 0) {
-    const int s = host_splits(hint.sel_pair, d->n_kv, lkv_host_read_inflight());
+    // At least kHostMinWgs workgroups in all, whatever the pair size. Measured on the 128K-token
+    // bf16 d128 step (8 KV heads), the PCIe rate depends on the count itself, not only on the
+    // bytes in flight: 8 workgroups per head gave 615-619 us/layer at 16-, 32- and 64-token
+    // blocks, 4 per head 641-645 at each of them, and 1 per head (64-token blocks) 652, under
+    // read budgets of 1-8 MiB.
+    int s = host_splits(hint.sel_pair, d->n_kv, lkv_host_read_inflight());
+    const int floor_s = (kHostMinWgs + d->n_kv - 1) / d->n_kv;
+    if (s < floor_s) s = floor_s;
     if (s < p.splits_a) {
       p.per_a = (p.n_a + s - 1) / s;
       p.splits_a = (p.n_a + p.per_a - 1) / p.per_a;
