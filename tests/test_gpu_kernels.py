@@ -292,6 +292,33 @@ def test_sparse_decode_matches_the_oracle(where: str, h: int, g: int, n: int, d:
     assert torch.equal(out_bf, out.to(torch.bfloat16)) and torch.equal(lse_bf, lse)
 
 
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_host_reads_of_large_blocks_take_the_workgroup_floor_and_match_the_oracle(bs: int) -> None:
+    """Selected pairs of 16-64 KiB read from host memory: the read budget alone would give 1-4
+    workgroups per KV head, the floor of 64 workgroups gives 8 here (98 items per head). Output and
+    LSE match the oracle, and the HBM launch over the same pool gives the same result to float32
+    summation order."""
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+
+    h, g, n, d, k, fill = 8, 4, 120, 128, 96, 5
+    w, pool = _pool_case(bs + 11, h, g, n, bs, d, torch.bfloat16)
+    store = pinned_empty(tuple(pool.shape), pool.dtype)
+    store.copy_(pool)
+    gen = torch.Generator().manual_seed(bs)
+    chosen = torch.stack([torch.randperm(n - 2, generator=gen)[:k] + 1 for _ in range(h)]).to(torch.int32)
+    scale = d**-0.5
+    outs = []
+    for src in (kernels.pool_source(store), kernels.pool_source(pool.cuda())):
+        outs.append(kernels.sparse_decode(w.query.cuda(), n_kv=h, block_size=bs, scale=scale, sel=src, idx=chosen.cuda(), sink=src, sink_block=0, cur=src, cur_block=n - 1, fill=fill, out_dtype=torch.float32))
+    torch.cuda.synchronize()
+    want_o, want_l = _oracle_decode(w.query, _f64(pool), chosen.numpy(), 0, n - 1, fill, scale, bs)
+    for out, lse in outs:
+        assert np.abs(out.cpu().numpy() - want_o).max() < TOL
+        assert np.abs(lse.cpu().numpy() - want_l).max() < TOL
+    assert (outs[0][0] - outs[1][0]).abs().max().item() < 1e-5
+
+
 @pytest.mark.parametrize(("d", "g", "dt"), [(128, 4, torch.bfloat16), (64, 4, torch.float16), (64, 2, torch.bfloat16), (128, 1, torch.float16)])
 def test_matrix_core_and_vector_scoring_agree(d: int, g: int, dt: torch.dtype) -> None:
     """HBM launches score on the matrix cores when the query has the pool's dtype and 16-byte
