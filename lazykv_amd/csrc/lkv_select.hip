@@ -44,6 +44,11 @@ constexpr int kPerThread = 12;                            // candidate keys held
 static_assert(kPerThread <= 32, "a thread's candidate slots are tracked in 32-bit masks");
 constexpr int kMaxCand = kSelThreads * kPerThread;        // 12288 candidates per KV head
 constexpr int kMaxSortedK = 2048;
+// Passes of the radix select. Each pass narrows the live key range to one bin of at most 2048:
+// a 32-bit range (width < 2^32) becomes < 2^21 wide, then < 2^10, then a single key value, and the
+// fourth pass finds lo == hi and stops. The loops are capped at this count, so a kernel whose
+// invariants were broken still ends (with the threshold it has) instead of spinning.
+constexpr int kRadixPasses = 4;
 
 __device__ __forceinline__ uint32_t orderable(float f) {
   uint32_t u = __float_as_uint(f);
@@ -225,8 +230,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
   uint32_t T;    // after the loop: take every key > T, `need` keys == T, and the marked keys
   uint32_t marked = 0u;  // bit u: key[u] lies in the final bin and ranks among the `need` best
   bool first_pass = true;
+  T = lo;  // kept only if the pass cap is reached, which the narrowing above rules out
 #pragma unroll 1
-  while (true) {
+  for (int pass = 0; pass < kRadixPasses; ++pass) {
     if (lo >= hi) {
       T = lo;
       break;
@@ -441,8 +447,9 @@ __global__ __launch_bounds__(kSelThreads) void select_stream_kernel(const float*
   int need = k;
   uint32_t T;
   bool ranked = false;  // the boundary bin was ranked directly: its best keys are marked in `taken`
+  T = lo;  // kept only if the pass cap is reached, which the narrowing rules out
 #pragma unroll 1
-  while (true) {
+  for (int pass = 0; pass < kRadixPasses; ++pass) {
     if (lo >= hi) {
       T = lo;
       break;

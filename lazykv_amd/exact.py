@@ -58,10 +58,6 @@ def partial_attention(
     return out.view(h, groups, d), lse.view(h, groups)
 
 
-# The reference's name: the pass it names now runs on the GPU.
-cpu_partial_attention = partial_attention
-
-
 # The reference's name for the cold partial (lazykv/exact.py:88-127). It runs on the GPU here, so
 # its tensors must be GPU tensors (or pinned host pools); CPU tensors are refused, not computed.
 cpu_partial_attention = partial_attention
