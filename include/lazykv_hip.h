@@ -175,7 +175,11 @@ int lkv_merge_lse(uintptr_t stream, const void* out_a, const float* lse_a, const
  * If kmin/kmax are not NULL, writes the per-channel key min/max of each block to
  * meta + h*meta_head_stride + b*d (meta_dtype): of the exact keys, or, for an int8 destination,
  * of the dequantised keys (lazykv/tiered.py:182-194,364-370). src may itself be
- * LKV_INT8_RECORD only when dst is NULL (metadata from existing records). */
+ * LKV_INT8_RECORD: with dst NULL it rebuilds the metadata of existing records; with a dst of the
+ * records' model dtype (src->deq_dtype) it dequantises each record into dst's layout (quant.py
+ * unpack, lazykv/quant.py:90-105) -- e.g. the sealed blocks of an int8 host tier read in place into
+ * a dense [1, h, T, d] buffer for a multi-token forward (lazykv/tiered.py:334-351 dense_kv, which
+ * the reference implements for the model-dtype tier only). */
 int lkv_store_blocks(uintptr_t stream, const lkv_kv_source* src, const lkv_kv_source* dst, int n_kv, int head_dim,
                      int block_size, int first_block, int n_blocks, void* kmin, void* kmax, int meta_dtype,
                      int64_t meta_head_stride);

@@ -14,7 +14,6 @@ scaled_dot_product_attention with the reference's lower-right causal alignment.
 from __future__ import annotations
 
 import math
-import time
 from dataclasses import dataclass
 
 import torch
@@ -90,7 +89,7 @@ def lazykv_attention_forward(
 
 @dataclass
 class KernelCheck:
-    """One strategy's startup verification (lazykv/attention.py:186-194)."""
+    """The start-up verification of one strategy (the reference's record, lazykv/attention.py:186-194)."""
 
     strategy: str
     ok: bool
@@ -101,75 +100,91 @@ class KernelCheck:
     error: str | None = None
 
 
-def _reference(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
-    """Float32 explicit attention with lower-right causal masking: the ground truth (:196-207)."""
-    q, k, v = query.float(), key.float(), value.float()
-    groups = q.shape[1] // k.shape[1]
-    k = k.repeat_interleave(groups, dim=1)
-    v = v.repeat_interleave(groups, dim=1)
-    scores = (q @ k.transpose(-1, -2).contiguous()) * scaling
-    q_len, kv_len = q.shape[-2], k.shape[-2]
-    q_pos = torch.arange(kv_len - q_len, kv_len, device=q.device)[:, None]
-    k_pos = torch.arange(kv_len, device=q.device)[None, :]
-    scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
-    return torch.softmax(scores, dim=-1) @ v
+def _truth(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
+    """Causal GQA attention in float64 on the host: query [1, n_q, q_len, d] at the last q_len
+    positions of key/value [1, kv, L, d]. Returns float64 [1, n_q, q_len, d] on the host."""
+    q = query.detach().double().cpu()[0]
+    k = key.detach().double().cpu()[0]
+    v = value.detach().double().cpu()[0]
+    n_q, q_len, _ = q.shape
+    n_kv, length, _ = k.shape
+    group = n_q // n_kv
+    out = torch.empty_like(q)
+    for head in range(n_q):
+        kh, vh = k[head // group], v[head // group]
+        logits = (q[head] @ kh.T) * scaling  # [q_len, L]
+        # Query row r sits at position L - q_len + r and sees keys 0 .. that position.
+        visible = torch.arange(length)[None, :] <= (length - q_len + torch.arange(q_len))[:, None]
+        logits = logits.masked_fill(~visible, float("-inf"))
+        out[head] = torch.softmax(logits, dim=-1) @ vh
+    return out.unsqueeze(0)
 
 
-def _rel_err(got: torch.Tensor, ref: torch.Tensor) -> float:
-    return ((got.float() - ref).abs().max() / ref.abs().max()).item()
+def _worst_rel(got: torch.Tensor, want: torch.Tensor) -> float:
+    """Largest absolute deviation relative to the largest output magnitude."""
+    g = got.detach().double().cpu()
+    return float((g - want).abs().max() / want.abs().max().clamp_min(1e-30))
 
 
-def _check_one(strategy: str, n_q: int, n_kv: int, head_dim: int, dtype: torch.dtype, probe_ctx: int, steps: int, tolerance: float) -> KernelCheck:
-    """Decode and chunked prefill against the float32 truth, with spare storage past the live
-    length as a preallocated cache has, then decode speed as the length grows by one per step
-    (lazykv/attention.py:214-245)."""
-    gen = torch.Generator(device="cuda").manual_seed(0)
+def _verify_hip(n_q: int, n_kv: int, head_dim: int, dtype: torch.dtype, probe_ctx: int, steps: int, tolerance: float) -> KernelCheck:
+    """The HIP decode and the chunked-prefill path against the float64 truth, over a preallocated
+    store whose rows past the live length hold large values (they must not be read), at live lengths
+    that end inside a block and on a block boundary; then the decode's device time, by events, as the
+    length grows one token per call from `probe_ctx`."""
+    rng = torch.Generator(device="cuda").manual_seed(1234)
     scaling = head_dim**-0.5
-
-    def rand(*shape: int) -> torch.Tensor:
-        return torch.randn(*shape, device="cuda", dtype=dtype, generator=gen)
-
+    spare = 48
     try:
-        store_k, store_v = rand(1, n_kv, 1024, head_dim), rand(1, n_kv, 1024, head_dim)
-        live = 509
-        k, v = store_k[:, :, :live], store_v[:, :, :live]
-        pq, dq = rand(1, n_q, 64, head_dim), rand(1, n_q, 1, head_dim)
-        err_p = _rel_err(attend(pq, k, v, scaling, strategy), _reference(pq, k, v, scaling))
-        err_d = _rel_err(attend(dq, k, v, scaling, strategy), _reference(dq, k, v, scaling))
-        big_k, big_v = rand(1, n_kv, probe_ctx + steps, head_dim), rand(1, n_kv, probe_ctx + steps, head_dim)
-        times = []
-        for i in range(steps):
-            length = probe_ctx + i
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            attend(dq, big_k[:, :, :length], big_v[:, :, :length], scaling, strategy)
-            torch.cuda.synchronize()
-            times.append(time.perf_counter() - t0)
+        worst_d, worst_p = 0.0, 0.0
+        for live in (DENSE_BLOCK - 1, 8 * DENSE_BLOCK, 8 * DENSE_BLOCK + 5, 600):
+            store = torch.randn((2, 1, n_kv, live + spare, head_dim), device="cuda", dtype=dtype, generator=rng)
+            store[:, :, :, live:] = 1e4
+            k, v = store[0, :, :, :live], store[1, :, :, :live]
+            for q_len in (1, 33):
+                if q_len > live:
+                    continue
+                q = torch.randn((1, n_q, q_len, head_dim), device="cuda", dtype=dtype, generator=rng)
+                err = _worst_rel(attend(q, k, v, scaling), _truth(q, k, v, scaling))
+                if q_len == 1:
+                    worst_d = max(worst_d, err)
+                else:
+                    worst_p = max(worst_p, err)
+        growing = torch.randn((2, 1, n_kv, probe_ctx + steps, head_dim), device="cuda", dtype=dtype, generator=rng)
+        q = torch.randn((1, n_q, 1, head_dim), device="cuda", dtype=dtype, generator=rng)
+        marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for i, (e0, e1) in enumerate(marks):
+            e0.record()
+            attend(q, growing[0, :, :, : probe_ctx + i], growing[1, :, :, : probe_ctx + i], scaling)
+            e1.record()
+        torch.cuda.synchronize()
+        took = sorted(e0.elapsed_time(e1) / 1e3 for e0, e1 in marks)
     except (RuntimeError, ValueError) as exc:
-        return KernelCheck(strategy, False, None, None, None, None, str(exc).splitlines()[0])
-    ok = math.isfinite(err_p) and math.isfinite(err_d) and max(err_p, err_d) <= tolerance
-    steady = sorted(times[1:])
-    return KernelCheck(strategy, ok, err_d, err_p, steady[len(steady) // 2], max(times))
+        return KernelCheck("hip", False, None, None, None, None, str(exc).splitlines()[0])
+    ok = math.isfinite(worst_d) and math.isfinite(worst_p) and max(worst_d, worst_p) <= tolerance
+    return KernelCheck("hip", ok, worst_d, worst_p, took[len(took) // 2], took[-1])
 
 
 def verify_strategies(n_q_heads: int, n_kv_heads: int, head_dim: int, dtype: torch.dtype = torch.bfloat16, tolerance: float = 1e-2,
                       probe_ctx: int = 16_000, steps: int = 24, candidates: tuple[str, ...] = STRATEGIES) -> list[KernelCheck]:
-    """Correctness (decode + chunked prefill vs float32) and growing-length decode speed (:248-266)."""
-    out = []
+    """Correctness of decode and chunked prefill, and growing-length decode speed, for each
+    candidate strategy (the reference's entry point, lazykv/attention.py:248-266). A strategy this
+    build does not have fails its check instead of raising."""
+    checks = []
     for name in candidates:
-        if name not in STRATEGIES:
-            out.append(KernelCheck(name, False, None, None, None, None, f"unknown strategy {name!r}: this build has {STRATEGIES}"))
-            continue
-        out.append(_check_one(name, n_q_heads, n_kv_heads, head_dim, dtype, probe_ctx, steps, tolerance))
-    return out
+        if name in STRATEGIES:
+            checks.append(_verify_hip(n_q_heads, n_kv_heads, head_dim, dtype, probe_ctx, steps, tolerance))
+        else:
+            checks.append(KernelCheck(name, False, None, None, None, None, f"unknown strategy {name!r}: this build has {STRATEGIES}"))
+    return checks
 
 
 def install(strategy: str | None = None, n_q_heads: int | None = None, n_kv_heads: int | None = None, head_dim: int | None = None,
             bucket: int = 0) -> tuple[str, list[KernelCheck]]:
     """Register the attention function with transformers under IMPLEMENTATION_NAME and pin the
     strategy (lazykv/attention.py:269-290). Given the model's head counts and head_dim, the
-    decode kernel is verified first against the float32 truth; a strategy that fails (or that
-    this build does not have) is a hard error, never a silent fallback."""
+    decode kernel and the chunked-prefill path are verified first against a float64 truth; a
+    strategy that fails (or that this build does not have) is a hard error, never a silent
+    fallback."""
     from transformers import AttentionInterface
 
     checks: list[KernelCheck] = []

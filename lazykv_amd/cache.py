@@ -1,9 +1,19 @@
-"""Preallocated per-layer KV stores (lazykv/cache.py:20-100): the dense layers' cache and the
-one-layer scratch that the layer-major prefill reuses for every selecting layer.
+"""Dense KV stores on the GPU: the layers that attend densely, and the prefill's one-layer scratch.
 
-A layer's KV lives in one zeroed [1, kv_heads, max_len, head_dim] pair allocated on its first
-update; `update` appends and returns views of the filled prefix only, so attention never scans
-unused rows (lazykv/cache.py:1-9,34-54). Batch size 1 only, as in the reference.
+The transformers `Cache` surface of the reference's dense store (`FullGPUCache`, its per-layer
+`PreallocatedLayer` and `CacheStats`, lazykv/cache.py:20-115) is kept, because `TieredCache`,
+`QuestView` and the snapshot reader take one. The storage is laid out for this build:
+
+* A layer's keys and values share one slab `[2, 1, h, capacity, d]` in HBM (`keys` is slab[0],
+  `values` slab[1]): one allocation per layer, made the first time the layer sees KV, so a layer
+  that never stores anything here (a tiered layer built by the layer-major prefill) holds no VRAM.
+* `update` appends along the token axis and returns views of the filled prefix `[1, h, n, d]`,
+  rows `d` elements apart: exactly the dense layout `kernels.dense_source` describes, so the decode
+  kernel reads this store in place.
+* The slab is zero-filled once. The HIP kernels never read rows past the live length, but a
+  consumer that masks unused rows by adding -inf would turn uninitialised NaN into NaN.
+
+Batch size 1, as in the reference.
 """
 
 from __future__ import annotations
@@ -23,10 +33,10 @@ class Decoded:
     lse: torch.Tensor
 
 
-@dataclass
+@dataclass(frozen=True)
 class CacheStats:
-    """Where a cache's KV lives (lazykv/cache.py:105-115): bytes resident in VRAM, bytes held only
-    in host memory, and the VRAM allocated for KV."""
+    """Where a cache's KV sits (the reference's `CacheStats`, lazykv/cache.py:105-115): bytes held
+    in VRAM, bytes held only in host memory, and the VRAM reserved for KV."""
 
     seq_len: int
     gpu_resident_kv_bytes: int
@@ -35,38 +45,58 @@ class CacheStats:
 
     @property
     def gpu_residency_fraction(self) -> float:
-        total = self.gpu_resident_kv_bytes + self.host_kv_bytes
-        return 1.0 if total == 0 else self.gpu_resident_kv_bytes / total
+        held = self.gpu_resident_kv_bytes + self.host_kv_bytes
+        return self.gpu_resident_kv_bytes / held if held else 1.0
 
 
-class PreallocatedLayer(CacheLayerMixin):
-    """One layer's KV in a preallocated tensor pair (lazykv/cache.py:20-70)."""
+class DenseLayer(CacheLayerMixin):
+    """One layer's KV in a single preallocated slab (the reference's `PreallocatedLayer`)."""
 
     def __init__(self, max_len: int, **kwargs: object) -> None:
         super().__init__()
+        if max_len <= 0:
+            raise ValueError(f"a dense layer needs a positive capacity, got {max_len}")
         self.max_len = max_len
         self.length = 0
+        self.slab: torch.Tensor | None = None
+
+    # -- storage ----------------------------------------------------------------------------------
 
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        b, h, _, d = key_states.shape
-        if b != 1:
-            raise ValueError("batch size 1 only")
+        if key_states.shape[0] != 1 or key_states.shape != value_states.shape:
+            raise ValueError(f"dense layers hold batch-1 KV with matching key/value shapes, got {tuple(key_states.shape)} / {tuple(value_states.shape)}")
+        _, h, _, d = key_states.shape
+        self.slab = torch.zeros((2, 1, h, self.max_len, d), dtype=key_states.dtype, device=key_states.device)
+        self.keys, self.values = self.slab[0], self.slab[1]
         self.dtype, self.device = key_states.dtype, key_states.device
-        # Zeroed once: rows past `length` are never read, but a zeroed pool cannot hold NaN.
-        self.keys = torch.zeros((1, h, self.max_len, d), dtype=key_states.dtype, device=key_states.device)
-        self.values = torch.zeros((1, value_states.shape[1], self.max_len, value_states.shape[3]), dtype=value_states.dtype, device=value_states.device)
         self.is_initialized = True
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args: object, **kwargs: object) -> tuple[torch.Tensor, torch.Tensor]:
         if not self.is_initialized:
             self.lazy_initialization(key_states, value_states)
-        end = self.length + key_states.shape[-2]
-        if end > self.max_len:
-            raise RuntimeError(f"KV cache overflow: {end} > max_len {self.max_len}")
-        self.keys[:, :, self.length : end].copy_(key_states)
-        self.values[:, :, self.length : end].copy_(value_states)
-        self.length = end
-        return self.keys[:, :, :end], self.values[:, :, :end]
+        a = self.length
+        b = a + key_states.shape[-2]
+        if b > self.max_len:
+            raise RuntimeError(f"dense layer full: appending {b - a} tokens to {a} exceeds its {self.max_len}-token capacity")
+        self.keys[:, :, a:b].copy_(key_states)
+        self.values[:, :, a:b].copy_(value_states)
+        self.length = b
+        return self.keys[:, :, :b], self.values[:, :, :b]
+
+    def _set_length(self, n: int) -> None:
+        if n < 0 or n > self.length:
+            raise ValueError(f"a dense layer of {self.length} tokens cannot be cut to {n}")
+        self.length = n
+
+    def reset(self) -> None:
+        """Forget every token; the slab is kept (only the live prefix is ever read)."""
+        self.length = 0
+
+    def truncate(self, length: int) -> None:
+        """Forget the tokens past `length`, so one prefill can be decoded from more than once."""
+        self._set_length(length)
+
+    # -- transformers plumbing --------------------------------------------------------------------
 
     def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
         return self.length + query_length, 0
@@ -77,27 +107,30 @@ class PreallocatedLayer(CacheLayerMixin):
     def get_max_length(self) -> int:
         return self.max_len
 
-    def reset(self) -> None:
-        self.length = 0
+    # -- accounting -------------------------------------------------------------------------------
 
-    def truncate(self, length: int) -> None:
-        if not 0 <= length <= self.length:
-            raise ValueError(f"cannot truncate length {self.length} to {length}")
-        self.length = length
+    def _token_bytes(self) -> int:
+        if self.slab is None:
+            return 0
+        _, _, h, _, d = self.slab.shape
+        return 2 * h * d * self.slab.element_size()
 
     def resident_bytes(self) -> int:
-        """KV bytes of the filled prefix (lazykv/cache.py:73-77)."""
-        if not self.is_initialized:
-            return 0
-        per_token = self.keys[0, :, 0].numel() * self.keys.element_size() + self.values[0, :, 0].numel() * self.values.element_size()
-        return per_token * self.length
+        """VRAM bytes of the live tokens' keys and values."""
+        return self._token_bytes() * self.length
+
+    def allocated_bytes(self) -> int:
+        return self._token_bytes() * self.max_len
+
+
+PreallocatedLayer = DenseLayer  # the reference's name for the per-layer store (lazykv/cache.py:20)
 
 
 class FullGPUCache(Cache):
-    """Every layer's KV resident on the GPU, preallocated (lazykv/cache.py:72-80)."""
+    """Every layer's KV held densely in VRAM (the reference's rung 1, lazykv/cache.py:80-102)."""
 
     def __init__(self, num_layers: int, max_len: int) -> None:
-        super().__init__(layers=[PreallocatedLayer(max_len) for _ in range(num_layers)])
+        super().__init__(layers=[DenseLayer(max_len) for _ in range(num_layers)])
         self.max_len = max_len
 
     def truncate(self, length: int) -> None:
@@ -105,18 +138,18 @@ class FullGPUCache(Cache):
             layer.truncate(length)
 
     def stats(self) -> CacheStats:
-        """Everything resident (lazykv/cache.py:91-102)."""
-        layers = [layer for layer in self.layers if isinstance(layer, PreallocatedLayer)]
-        resident = sum(layer.resident_bytes() for layer in layers)
-        allocated = sum(layer.keys.numel() * layer.keys.element_size() + layer.values.numel() * layer.values.element_size()
-                        for layer in layers if layer.is_initialized)
-        return CacheStats(seq_len=layers[0].get_seq_length() if layers else 0, gpu_resident_kv_bytes=resident, host_kv_bytes=0,
-                          gpu_allocated_kv_bytes=allocated)
+        dense = [layer for layer in self.layers if isinstance(layer, DenseLayer)]
+        return CacheStats(
+            seq_len=dense[0].get_seq_length() if dense else 0,
+            gpu_resident_kv_bytes=sum(layer.resident_bytes() for layer in dense),
+            host_kv_bytes=0,
+            gpu_allocated_kv_bytes=sum(layer.allocated_bytes() for layer in dense),
+        )
 
     @classmethod
     def from_kv(cls, layers: list[tuple[torch.Tensor, torch.Tensor]], max_len: int) -> FullGPUCache:
         """A cache holding copies of per-layer prompt KV [1, h, L, d]."""
-        full = cls(len(layers), max_len)
-        for store, (k, v) in zip(full.layers, layers):
-            store.update(k, v)
-        return full
+        cache = cls(len(layers), max_len)
+        for dense, (k, v) in zip(cache.layers, layers):
+            dense.update(k, v)
+        return cache

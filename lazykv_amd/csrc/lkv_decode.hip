@@ -1423,3 +1423,4 @@ extern "C" int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, 
   return sparse_decode_impl(stream, desc, q, q_dtype, host, idx, idx_stride, sink, cur, nullptr, out, out_dtype, lse, ws,
                             dec_bytes, slots, loc, (int64_t)d.k, &res);
 }
+

@@ -19,7 +19,14 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 
-enum { MODE_META = 0, MODE_COPY = 1, MODE_INT8 = 2, MODE_META_FROM_I8 = 3 };
+// What a launch does with each pair:
+//   MODE_META          metadata of the exact keys only;
+//   MODE_COPY          model-dtype pair copied to dst (+ metadata of the exact keys);
+//   MODE_INT8          int8 record of the pair written to dst (+ metadata of the dequantised keys);
+//   MODE_META_FROM_I8  metadata of an existing record's dequantised keys;
+//   MODE_UNPACK        an existing record dequantised into a model-dtype pair of dst (+ metadata of
+//                      those keys): quant.py unpack into any block layout.
+enum { MODE_META = 0, MODE_COPY = 1, MODE_INT8 = 2, MODE_META_FROM_I8 = 3, MODE_UNPACK = 4 };
 
 struct StoreArgs {
   const void* sk;
@@ -117,10 +124,19 @@ __device__ __forceinline__ void store_pair(const StoreArgs& a, int64_t pair) {
   const int rows = bs >> 2;  // rows per row group
   const bool want_meta = a.kmin != nullptr;
 
-  if constexpr (MODE == MODE_META_FROM_I8) {
-    // Metadata of the dequantised keys of an existing record.
+  if constexpr (MODE == MODE_META_FROM_I8 || MODE == MODE_UNPACK) {
+    // An existing record: the metadata of its dequantised keys and, for MODE_UNPACK, the pair
+    // itself dequantised into dst (quant.py:103-105: ((q + 128) * scale) + zero, two separately
+    // rounded float32 operations, then the model dtype).
     const uint8_t* rec = (const uint8_t*)a.sk + (int64_t)b * a.s_bstride + (int64_t)h * a.s_hstride;
     const uint16_t* sc = (const uint16_t*)(rec + 2 * bs * D);
+    T* dk = nullptr;
+    T* dv = nullptr;
+    if constexpr (MODE == MODE_UNPACK) {
+      const int64_t doff = (int64_t)b * a.d_bstride + (int64_t)h * a.d_hstride + c * EPL;
+      dk = (T*)a.dk + doff;
+      dv = (T*)a.dv + doff;
+    }
     float ks[EPL], kz[EPL], mn[EPL], mx[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
@@ -130,15 +146,29 @@ __device__ __forceinline__ void store_pair(const StoreArgs& a, int64_t pair) {
       mx[e] = -INFINITY;
     }
     for (int i = 0; i < rows; ++i) {
+      const int row = r + 4 * i;
       int8_t q[EPL];
-      load_bytes<EPL>((const int8_t*)rec + (r + 4 * i) * D + c * EPL, q);
+      load_bytes<EPL>((const int8_t*)rec + row * D + c * EPL, q);
+      float x[EPL];
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
-        const float x = lkv::round_through<MT>(((float)q[e] + 128.0f) * ks[e] + kz[e]);
-        mn[e] = fminf(mn[e], x);
-        mx[e] = fmaxf(mx[e], x);
+        x[e] = lkv::round_through<MT>(((float)q[e] + 128.0f) * ks[e] + kz[e]);
+        mn[e] = fminf(mn[e], x[e]);
+        mx[e] = fmaxf(mx[e], x[e]);
+      }
+      if constexpr (MODE == MODE_UNPACK) {
+        store_segment<MT, EPL>(dk + (int64_t)row * D, x);
+        int8_t vq[EPL];
+        load_bytes<EPL>((const int8_t*)rec + bs * D + row * D + c * EPL, vq);
+        const float vs = lkv::f16_to_f32(sc[2 * D + row]);
+        const float vz = lkv::f16_to_f32(sc[2 * D + bs + row]);
+        float v[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[e] = ((float)vq[e] + 128.0f) * vs + vz;
+        store_segment<MT, EPL>(dv + (int64_t)row * D, v);
       }
     }
+    if (!want_meta) return;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
       mn[e] = lkv::groups4_min(mn[e]);
@@ -263,45 +293,6 @@ __global__ __launch_bounds__(kThreads) void store_blocks_kernel(StoreArgs a) {
     store_pair<D, MT, MODE>(a, pair);  // `pair` is wave-uniform
 }
 
-// quant.py unpack: records [m, P] -> pairs [m, 2, bs, D] in the model dtype.
-template <int D, int MT>
-__global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t* __restrict__ records, int64_t m, int bs,
-                                                          typename lkv::Elem<MT>::T* __restrict__ out) {
-  using T = typename lkv::Elem<MT>::T;
-  constexpr int EPL = D / 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane >> 4, c = lane & 15;
-  const int64_t i_rec = (int64_t)blockIdx.x * kWaves + wave;
-  if (i_rec >= m) return;
-  const int64_t P = 2LL * bs * D + 4LL * D + 4LL * bs;
-  const uint8_t* rec = records + i_rec * P;
-  const uint16_t* sc = (const uint16_t*)(rec + 2 * bs * D);
-  T* ok = out + i_rec * 2LL * bs * D;
-  T* ov = ok + (int64_t)bs * D;
-  float ks[EPL], kz[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    ks[e] = lkv::f16_to_f32(sc[c * EPL + e]);
-    kz[e] = lkv::f16_to_f32(sc[D + c * EPL + e]);
-  }
-  for (int i = 0; i < (bs >> 2); ++i) {
-    const int row = r + 4 * i;
-    int8_t kq[EPL], vq[EPL];
-    load_bytes<EPL>((const int8_t*)rec + row * D + c * EPL, kq);
-    load_bytes<EPL>((const int8_t*)rec + bs * D + row * D + c * EPL, vq);
-    const float vs = lkv::f16_to_f32(sc[2 * D + row]);
-    const float vz = lkv::f16_to_f32(sc[2 * D + bs + row]);
-    float k[EPL], v[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      k[e] = ((float)kq[e] + 128.0f) * ks[e] + kz[e];
-      v[e] = ((float)vq[e] + 128.0f) * vs + vz;
-    }
-    store_segment<MT, EPL>(ok + (int64_t)row * D + c * EPL, k);
-    store_segment<MT, EPL>(ov + (int64_t)row * D + c * EPL, v);
-  }
-}
-
 template <int D, int MT>
 int launch_store(hipStream_t s, int mode, const StoreArgs& a, int64_t max_wgs) {
   const int64_t pairs = (int64_t)a.n_blocks * a.n_kv;
@@ -312,6 +303,7 @@ int launch_store(hipStream_t s, int mode, const StoreArgs& a, int64_t max_wgs) {
     case MODE_META: hipLaunchKernelGGL((store_blocks_kernel<D, MT, MODE_META>), grid, dim3(kThreads), 0, s, a); break;
     case MODE_COPY: hipLaunchKernelGGL((store_blocks_kernel<D, MT, MODE_COPY>), grid, dim3(kThreads), 0, s, a); break;
     case MODE_INT8: hipLaunchKernelGGL((store_blocks_kernel<D, MT, MODE_INT8>), grid, dim3(kThreads), 0, s, a); break;
+    case MODE_UNPACK: hipLaunchKernelGGL((store_blocks_kernel<D, MT, MODE_UNPACK>), grid, dim3(kThreads), 0, s, a); break;
     default:
       hipLaunchKernelGGL((store_blocks_kernel<D, MT, MODE_META_FROM_I8>), grid, dim3(kThreads), 0, s, a);
       break;
@@ -349,10 +341,15 @@ extern "C" int lkv_store_blocks(uintptr_t stream, const lkv_kv_source* src, cons
   int mode;
   int mt;
   if (src->dtype == LKV_INT8_RECORD) {
-    LKV_CHECK_ARG(dst == nullptr, "an int8 source only rebuilds metadata (dst must be NULL)");
-    LKV_CHECK_ARG(kmin != nullptr, "nothing to do");
-    mode = MODE_META_FROM_I8;
     mt = src->deq_dtype;
+    if (dst == nullptr) {
+      LKV_CHECK_ARG(kmin != nullptr, "nothing to do");
+      mode = MODE_META_FROM_I8;
+    } else {
+      LKV_CHECK_ARG(dst->dtype == mt && dst->k != nullptr && dst->v != nullptr,
+                    "int8 records dequantise into a destination of their model dtype");
+      mode = MODE_UNPACK;
+    }
   } else {
     LKV_CHECK_ARG(lkv_is_model_dtype(src->dtype) && src->v != nullptr, "bad source");
     mt = src->dtype;
@@ -424,22 +421,11 @@ extern "C" int lkv_unpack_int8(uintptr_t stream, const void* records, int64_t m,
   LKV_CHECK_ARG(block_size >= 4 && block_size <= 256 && block_size % 4 == 0,
                 "block_size %d unsupported (a multiple of 4 up to 256)", block_size);
   LKV_CHECK_ARG(lkv_is_model_dtype(dtype), "bad dtype");
-  if (m == 0) return LKV_OK;
-  hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)((m + kWaves - 1) / kWaves));
-#define LKV_UNPACK(D, MT)                                                                                       \
-  hipLaunchKernelGGL((unpack_kernel<D, MT>), grid, dim3(kThreads), 0, s, (const uint8_t*)records, m, block_size, \
-                     (typename lkv::Elem<MT>::T*)pairs)
-  if (head_dim == 128) {
-    if (dtype == LKV_BF16) LKV_UNPACK(128, LKV_BF16);
-    else if (dtype == LKV_F16) LKV_UNPACK(128, LKV_F16);
-    else LKV_UNPACK(128, LKV_F32);
-  } else {
-    if (dtype == LKV_BF16) LKV_UNPACK(64, LKV_BF16);
-    else if (dtype == LKV_F16) LKV_UNPACK(64, LKV_F16);
-    else LKV_UNPACK(64, LKV_F32);
-  }
-#undef LKV_UNPACK
-  LKV_CHECK_LAUNCH("unpack_int8");
-  return LKV_OK;
+  LKV_CHECK_ARG(m <= 0x7fffffff, "bad record count");
+  // Records [m, P] as m blocks of one head, dequantised into pairs [m, 2, bs, d].
+  const int64_t pair_elems = 2LL * block_size * head_dim;
+  lkv_kv_source src{records, nullptr, lkv_packed_pair_bytes(block_size, head_dim), 0, m, LKV_INT8_RECORD, dtype, 0};
+  lkv_kv_source dst{pairs, (const char*)pairs + (int64_t)block_size * head_dim * lkv_dtype_size(dtype), pair_elems, 0, m,
+                    dtype, dtype, 0};
+  return lkv_store_blocks(stream, &src, &dst, 1, head_dim, block_size, 0, (int)m, nullptr, nullptr, dtype, 0);
 }

@@ -1,20 +1,24 @@
-"""Session snapshots of a tiered cache, in the reference's file format (lazykv/snapshot.py:16-20).
+"""Session snapshots of a tiered cache in the reference's on-disk format (lazykv/snapshot.py:16-20).
 
-A sealed block never changes once it is in the host pool, so a snapshot is the pool as it is, plus
-what is still only on the GPU (the dense layers' KV, each tiered layer's unsealed tail) and the
-logits for the next token.
+A sealed block never changes once it is in the host pool, so a snapshot is the pool's bytes as they
+are, plus what lives only on the GPU -- the dense layers' KV and each tiered layer's unsealed tail
+-- and the logits for the next token.
 
-File layout (lazykv/snapshot.py:16-20,67-114): an 8-byte little-endian header length, a JSON
-header, zero padding to ALIGN, then sections each starting at a multiple of ALIGN -- the
-next-token logits (float32), then per layer either `L{i}.kv` [2, h, L, d] (a dense layer) or
-`L{i}.blocks`, the host pool's own [B, h, 2, bs, d] bytes, and `L{i}.tail` [h, 2, fill, d] (a
-tiered layer). Offsets in the header are relative to the first section. The same magic string and
-layout as the reference, so either side reads the other's files.
+Format (kept byte-compatible with the reference, so either side reads the other's files): an
+8-byte little-endian header length, the JSON header (magic "lazykv-snapshot-1", length,
+block_size, dense_layers, heads, head_dim, dtype, vocab, per-layer kinds, and `sections`: name ->
+[offset, bytes] relative to the first section), zero padding to ALIGN = 4096, then the sections,
+each starting on a multiple of ALIGN: `logits` (float32), then per layer `L{i}.kv` [2, h, L, d]
+for a dense layer, or `L{i}.blocks` (the host pool's own [B, h, 2, bs, d] bytes) and `L{i}.tail`
+[h, 2, fill, d] for a tiered one.
 
-Restore ("store", lazykv/snapshot.py:219-231): each tiered layer's sealed blocks are read straight
-into its mapped host pool; the GPU then reads the pool in place to rebuild the block metadata
-(`TieredLayer.from_store`), so no KV byte crosses the link twice. ("boundary" instead copies the
-layer to the GPU and builds the tier as the prefill boundary does, lazykv/snapshot.py:232-239.)
+I/O here is positioned: the file is sized once (the gaps read back as zeros, the padding the
+format asks for), each section is written with `os.pwrite` straight from its memory -- the mapped
+pinned host pool needs no staging copy -- and restore reads each section with `os.preadv` straight
+into its destination, the blocks into the layer's mapped host pool. With `rebuild="store"` the GPU
+then rebuilds that layer's metadata by reading the pool in place (`TieredLayer.from_store`) while
+the host reads the next layer; `rebuild="boundary"` instead hands the layer's dense KV to the tier
+constructor, as a prefill's boundary would (lazykv/snapshot.py:219-239).
 """
 
 from __future__ import annotations
@@ -24,7 +28,7 @@ import os
 import time
 from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Any, BinaryIO
+from typing import Any
 
 import torch
 
@@ -34,103 +38,132 @@ from lazykv_amd.tiered import TieredCache, TieredLayer
 
 MAGIC = "lazykv-snapshot-1"
 ALIGN = 4096
-_DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+_HEADER_MAX = 1 << 30  # a header length beyond this is not a snapshot
+_DTYPE_NAMES = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}
+_NAMED_DTYPES = {name: dt for dt, name in _DTYPE_NAMES.items()}
 
 
 def _pad(n: int) -> int:
-    return -(-n // ALIGN) * ALIGN
+    """`n` rounded up to the section alignment."""
+    return (n + ALIGN - 1) // ALIGN * ALIGN
 
 
-def _bytes(t: torch.Tensor) -> memoryview:
-    """A CPU tensor's bytes (bfloat16 has no numpy dtype, so through a uint8 view)."""
-    t = t.contiguous()
+def _raw(t: torch.Tensor) -> memoryview:
+    """The bytes of a contiguous CPU tensor, aliased (bfloat16 has no numpy type: via uint8)."""
+    if not t.is_contiguous():
+        raise ValueError("snapshot sections are contiguous tensors")
     return memoryview(t.view(torch.uint8).reshape(-1).numpy())
 
 
 @dataclass
 class SaveStats:
     bytes_written: int
-    seconds: float  # fsync included
+    seconds: float  # until the file is on disk (fsync included)
 
 
 @dataclass
 class RestoreStats:
     bytes_read: int
     read_s: float
-    rebuild_s: float  # everything but the reads: H2D, metadata, slots, dense layers, the final sync
+    rebuild_s: float  # everything but the reads: the GPU rebuild, dense layers, the final sync
     sections: dict[str, float] = field(default_factory=dict)
 
 
+class _Sections:
+    """Section names, sizes and aligned offsets, in file order."""
+
+    def __init__(self) -> None:
+        self.order: list[tuple[str, torch.Tensor]] = []
+        self.table: dict[str, list[int]] = {}
+        self.end = 0
+
+    def add(self, name: str, t: torch.Tensor) -> None:
+        n = t.numel() * t.element_size()
+        self.table[name] = [self.end, n]
+        self.order.append((name, t))
+        self.end += _pad(n)
+
+
 def save(cache: TieredCache, next_logits: torch.Tensor, path: Path) -> SaveStats:
-    """Write `cache` at its current position and the logits for its next token (lazykv/snapshot.py:67-114)."""
+    """Write `cache` at its current position and the logits for its next token
+    (lazykv/snapshot.py:67-114). The int8 tier is refused, as in the reference."""
     if cache.quant is not None:
-        raise ValueError("snapshots of the int8 tier are not supported")
+        raise ValueError("snapshots hold model-dtype pairs; the int8 tier is not supported")
     t0 = time.perf_counter()
     torch.cuda.synchronize()
     tiers = cache.tiers
-    any_tier = next(iter(tiers.values()))
-    length = any_tier.length
-    sections: list[tuple[str, torch.Tensor]] = [("logits", next_logits.float().cpu())]
-    layers: list[dict[str, Any]] = []
-    for i in range(len(cache.full.layers)):
-        if i in tiers:
-            t = tiers[i]
-            if t.length != length:
-                raise RuntimeError("tiered layers disagree on length")
-            blocks = t.host[: t.n_sealed] if t.host is not None else t.store[: t.n_sealed].cpu()
-            sections.append((f"L{i}.blocks", blocks))
-            sections.append((f"L{i}.tail", t.pool[t.tail_slot, :, :, : t.fill].cpu()))  # [h, 2, fill, d]
-            layers.append({"kind": "tier", "n_sealed": t.n_sealed, "fill": t.fill})
-        else:
-            src = cache.full.layers[i]
-            if src.get_seq_length() != length:
-                raise RuntimeError(f"dense layer {i} has length {src.get_seq_length()}, the tier {length}")
-            sections.append((f"L{i}.kv", torch.stack([src.keys[0, :, :length], src.values[0, :, :length]]).cpu()))  # [2, h, L, d]
-            layers.append({"kind": "dense"})
-    offsets, cursor = {}, 0
-    for name, t in sections:
-        offsets[name] = [cursor, t.numel() * t.element_size()]
-        cursor += _pad(offsets[name][1])
+    probe = next(iter(tiers.values()))
+    length = probe.length
+    sec = _Sections()
+    sec.add("logits", next_logits.detach().float().cpu().contiguous())
+    kinds: list[dict[str, Any]] = []
+    for i, layer in enumerate(cache.full.layers):
+        t = tiers.get(i)
+        if t is None:
+            if layer.get_seq_length() != length:
+                raise RuntimeError(f"dense layer {i} holds {layer.get_seq_length()} tokens, the tiers {length}")
+            kv = torch.stack([layer.keys[0, :, :length], layer.values[0, :, :length]]).cpu()  # [2, h, L, d]
+            sec.add(f"L{i}.kv", kv)
+            kinds.append({"kind": "dense"})
+            continue
+        if t.length != length:
+            raise RuntimeError(f"tiered layer {i} holds {t.length} tokens, layer {next(iter(tiers))} {length}")
+        # The pool is mapped host memory: written from where it lies. An HBM store is copied down.
+        blocks = t.host[: t.n_sealed] if t.host is not None else t.store[: t.n_sealed].cpu()
+        sec.add(f"L{i}.blocks", blocks)
+        sec.add(f"L{i}.tail", t.pool[1, :, :, : t.fill].cpu().contiguous())
+        kinds.append({"kind": "tier", "n_sealed": t.n_sealed, "fill": t.fill})
     header = {
         "magic": MAGIC, "length": length, "block_size": cache.block_size, "dense_layers": cache.dense_layers,
-        "heads": any_tier.h, "head_dim": any_tier.d, "dtype": str(any_tier.pool.dtype).removeprefix("torch."),
-        "vocab": int(next_logits.numel()), "layers": layers, "sections": offsets,
+        "heads": probe.h, "head_dim": probe.d, "dtype": _DTYPE_NAMES[probe.dtype],
+        "vocab": int(next_logits.numel()), "layers": kinds, "sections": sec.table,
     }
-    head = json.dumps(header).encode()
-    base = _pad(len(head) + 8)
+    text = json.dumps(header).encode()
+    base = _pad(8 + len(text))
+    total = base + sec.end
     path = Path(path)
     path.parent.mkdir(parents=True, exist_ok=True)
-    with path.open("wb") as f:
-        f.write(len(head).to_bytes(8, "little") + head)
-        f.write(b"\0" * (base - len(head) - 8))
-        for _, t in sections:
-            n = f.write(_bytes(t))
-            f.write(b"\0" * (_pad(n) - n))
-        f.flush()
-        os.fsync(f.fileno())
-    return SaveStats(base + cursor, time.perf_counter() - t0)
+    fd = os.open(path, os.O_WRONLY | os.O_CREAT | os.O_TRUNC, 0o644)
+    try:
+        os.ftruncate(fd, total)  # every byte not written below reads back as zero
+        _pwrite_all(fd, memoryview(len(text).to_bytes(8, "little") + text), 0)
+        for name, t in sec.order:
+            _pwrite_all(fd, _raw(t), base + sec.table[name][0])
+        os.fsync(fd)
+    finally:
+        os.close(fd)
+    return SaveStats(total, time.perf_counter() - t0)
+
+
+def _pwrite_all(fd: int, data: memoryview, offset: int) -> None:
+    done = 0
+    while done < len(data):
+        done += os.pwrite(fd, data[done:], offset + done)
+
+
+def _pread_into(fd: int, dst: memoryview, offset: int) -> None:
+    done = 0
+    while done < len(dst):
+        got = os.preadv(fd, [dst[done:]], offset + done)
+        if got <= 0:
+            raise EOFError(f"snapshot ends early: {done} of {len(dst)} bytes at offset {offset}")
+        done += got
 
 
 def read_header(path: Path) -> tuple[dict[str, Any], int]:
     """(header, byte offset of the first section); ValueError for a file that is not a snapshot."""
     with Path(path).open("rb") as f:
-        raw = f.read(8)
-        n = int.from_bytes(raw, "little") if len(raw) == 8 else -1
-        try:
-            header = json.loads(f.read(n)) if 0 < n < (1 << 30) else None
-        except ValueError:
-            header = None
+        prefix = f.read(8)
+        size = int.from_bytes(prefix, "little") if len(prefix) == 8 else 0
+        header: Any = None
+        if 0 < size < _HEADER_MAX:
+            try:
+                header = json.loads(f.read(size))
+            except (ValueError, UnicodeDecodeError):
+                header = None
     if not isinstance(header, dict) or header.get("magic") != MAGIC:
         raise ValueError(f"{path} is not a LazyKV snapshot")
-    return header, _pad(n + 8)
-
-
-def _read_into(f: BinaryIO, offset: int, out: torch.Tensor) -> None:
-    f.seek(offset)
-    view = _bytes(out)  # `out` is contiguous: this aliases its memory
-    got = f.readinto(view)
-    if got != len(view):
-        raise EOFError(f"short read: {got} of {len(view)} bytes at offset {offset}")
+    return header, _pad(8 + size)
 
 
 def restore(
@@ -148,68 +181,74 @@ def restore(
     """A TieredCache at the snapshot's position and the logits for its next token
     (lazykv/snapshot.py:184-278). `tier_kwargs` (exact, rank_dtype) go to the tiers and the cache."""
     if rebuild not in ("store", "boundary"):
-        raise ValueError(f"unknown rebuild {rebuild!r}")
+        raise ValueError(f"rebuild must be 'store' or 'boundary', got {rebuild!r}")
     header, base = read_header(path)
-    dt = _DTYPES[header["dtype"]]
+    dtype = _NAMED_DTYPES[header["dtype"]]
     h, d, bs, length = header["heads"], header["head_dim"], header["block_size"], header["length"]
-    if len(header["layers"]) != num_layers:
-        raise ValueError(f"snapshot has {len(header['layers'])} layers, the model {num_layers}")
+    specs = header["layers"]
+    if len(specs) != num_layers:
+        raise ValueError(f"the snapshot has {len(specs)} layers, the model {num_layers}")
     if length > capacity_tokens:
-        raise ValueError(f"snapshot of {length} tokens exceeds capacity {capacity_tokens}")
-    sec = header["sections"]
+        raise ValueError(f"the snapshot's {length} tokens exceed capacity {capacity_tokens}")
+    if sum(s["kind"] == "dense" for s in specs) != header["dense_layers"]:
+        raise ValueError("the snapshot's dense layer count disagrees with its header")
+    table = header["sections"]
     stats = RestoreStats(0, 0.0, 0.0)
+    device = torch.device("cuda", torch.cuda.current_device())
+    layer_kw = {key: tier_kwargs[key] for key in ("exact", "rank_dtype") if key in tier_kwargs}
+    cap_blocks = -(-capacity_tokens // bs)
     full = FullGPUCache(num_layers, capacity_tokens)
     tiers: dict[int, TieredLayer] = {}
-    dense = 0
-    dev = torch.device("cuda", torch.cuda.current_device())
-    layer_kw = {key: tier_kwargs[key] for key in ("exact", "rank_dtype") if key in tier_kwargs}
-    with Path(path).open("rb", buffering=0) as f:
+    fd = os.open(path, os.O_RDONLY)
 
-        def load(name: str, shape: tuple[int, ...], dtype: torch.dtype, into: torch.Tensor | None = None) -> torch.Tensor:
-            out = torch.empty(shape, dtype=dtype) if into is None else into
-            if out.numel() * out.element_size() != sec[name][1]:
-                raise ValueError(f"section {name} holds {sec[name][1]} bytes, expected {out.numel() * out.element_size()}")
-            t0 = time.perf_counter()
-            _read_into(f, base + sec[name][0], out)
-            stats.read_s += time.perf_counter() - t0
-            stats.bytes_read += sec[name][1]
-            return out
+    def section(name: str, out: torch.Tensor) -> torch.Tensor:
+        """Read section `name` into the contiguous CPU tensor `out` (pinned pools included)."""
+        want = out.numel() * out.element_size()
+        if table[name][1] != want:
+            raise ValueError(f"section {name} holds {table[name][1]} bytes where {want} are expected")
+        r0 = time.perf_counter()
+        _pread_into(fd, _raw(out), base + table[name][0])
+        dt = time.perf_counter() - r0
+        stats.read_s += dt
+        stats.sections[name] = dt
+        stats.bytes_read += want
+        return out
 
-        logits = load("logits", (header["vocab"],), torch.float32).to(dev)
-        for i, spec in enumerate(header["layers"]):
+    try:
+        logits = section("logits", torch.empty(header["vocab"], dtype=torch.float32)).to(device)
+        tiered_seen = 0
+        for i, spec in enumerate(specs):
             if spec["kind"] == "dense":
-                kv = load(f"L{i}.kv", (2, h, length, d), dt)
-                t0 = time.perf_counter()
-                g = kv.to(dev)
-                full.layers[i].update(g[0:1], g[1:2])
-                stats.rebuild_s += time.perf_counter() - t0
-                dense += 1
+                kv = section(f"L{i}.kv", torch.empty((2, h, length, d), dtype=dtype))
+                g0 = time.perf_counter()
+                on_gpu = kv.to(device)
+                full.layers[i].update(on_gpu[0:1], on_gpu[1:2])
+                stats.rebuild_s += time.perf_counter() - g0
                 continue
             n, fill = spec["n_sealed"], spec["fill"]
-            host = None if host_pools is None else host_pools[i - header["dense_layers"]]
+            pool = host_pools[tiered_seen] if host_pools is not None else None
+            tiered_seen += 1
             if rebuild == "store":
-                t0 = time.perf_counter()
-                if host is None:
-                    host = pinned_empty((-(-capacity_tokens // bs), h, 2, bs, d), dt)
-                stats.rebuild_s += time.perf_counter() - t0
-                load(f"L{i}.blocks", (n, h, 2, bs, d), dt, into=host[:n])
-                tail = load(f"L{i}.tail", (h, 2, fill, d), dt)
-                t0 = time.perf_counter()
-                tiers[i] = TieredLayer.from_store(host, n, tail, k_blocks, bs, capacity_tokens, dev, n_slots, fetch=fetch, **layer_kw)
-                stats.rebuild_s += time.perf_counter() - t0
-                continue
-            blocks = load(f"L{i}.blocks", (n, h, 2, bs, d), dt)
-            tail = load(f"L{i}.tail", (h, 2, fill, d), dt)
-            t0 = time.perf_counter()
-            g = blocks.to(dev).permute(1, 2, 0, 3, 4).reshape(h, 2, n * bs, d)  # [h, 2, B*bs, d]
-            kv = torch.cat([g, tail.to(dev)], dim=2)
-            tiers[i] = TieredLayer(kv[None, :, 0], kv[None, :, 1], k_blocks, bs, capacity_tokens, host, n_slots, fetch=fetch, **layer_kw)
-            del g, kv
-            stats.rebuild_s += time.perf_counter() - t0
-    if dense != header["dense_layers"]:
-        raise ValueError("snapshot's dense layer count disagrees with its header")
-    t0 = time.perf_counter()
-    cache = TieredCache(full, k_blocks, bs, capacity_tokens, model=model, dense_layers=dense, n_slots=n_slots, fetch=fetch, tiers=tiers, **tier_kwargs)
+                if pool is None:
+                    pool = pinned_empty((cap_blocks, h, 2, bs, d), dtype)
+                section(f"L{i}.blocks", pool[:n])
+                tail = section(f"L{i}.tail", torch.empty((h, 2, fill, d), dtype=dtype)).to(device)
+                g0 = time.perf_counter()
+                tiers[i] = TieredLayer.from_store(pool, n, tail, k_blocks, bs, capacity_tokens, device, n_slots, fetch=fetch, **layer_kw)
+                stats.rebuild_s += time.perf_counter() - g0
+            else:
+                blocks = section(f"L{i}.blocks", torch.empty((n, h, 2, bs, d), dtype=dtype))
+                tail = section(f"L{i}.tail", torch.empty((h, 2, fill, d), dtype=dtype))
+                g0 = time.perf_counter()
+                # [n, h, 2, bs, d] -> per head and side, the tokens in order: [2, h, n*bs + fill, d]
+                seq = blocks.to(device).permute(2, 1, 0, 3, 4).reshape(2, h, n * bs, d)
+                kv = torch.cat([seq, tail.to(device).permute(1, 0, 2, 3)], dim=2)
+                tiers[i] = TieredLayer(kv[0:1], kv[1:2], k_blocks, bs, capacity_tokens, pool, n_slots, fetch=fetch, **layer_kw)
+                stats.rebuild_s += time.perf_counter() - g0
+    finally:
+        os.close(fd)
+    g0 = time.perf_counter()
+    cache = TieredCache(full, k_blocks, bs, capacity_tokens, model=model, dense_layers=header["dense_layers"], n_slots=n_slots, fetch=fetch, tiers=tiers, **tier_kwargs)
     torch.cuda.synchronize()
-    stats.rebuild_s += time.perf_counter() - t0
+    stats.rebuild_s += time.perf_counter() - g0
     return cache, logits, stats

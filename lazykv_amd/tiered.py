@@ -54,7 +54,40 @@ class TierCounters:
     seals: int = 0
     seal_bytes: int = 0
     boundary_d2h_bytes: int = 0
+    # Dense ingestion of multi-token forwards (lazykv/tiered.py:101-104,649-663).
+    ingest_forwards: int = 0
+    ingest_tokens: int = 0
+    ingest_h2d_bytes: int = 0
     fetched_pairs_per_step: list[int] = field(default_factory=list)
+
+
+def _renumbered(src: kernels.Source, first: int, elem_bytes: int) -> kernels.Source:
+    """`src` with its block 0 addressed as block `first`: a store of blocks [first, first + n)
+    then reads the source's blocks [0, n). The base addresses move back by `first` blocks; the
+    kernel only addresses blocks from `first` on, which lie inside the source."""
+    back = first * src.block_stride * (1 if src.dtype == _lib.INT8_RECORD else elem_bytes)
+    return kernels.Source(src.k - back, src.v - back if src.v else 0, src.block_stride, src.head_stride, src.dtype, src.deq_dtype,
+                          first + src.n_blocks, src.owners, src.flags)
+
+
+class DenseScratch:
+    """One HBM buffer pair [1, h, T, d] that a multi-token forward's dense keys and values are
+    assembled in (`TieredLayer.dense_kv`). A cache's selecting layers run one after another on one
+    stream, so they share it; it grows to the longest forward seen and is never shrunk."""
+
+    def __init__(self) -> None:
+        self.k: torch.Tensor | None = None
+        self.v: torch.Tensor | None = None
+
+    def take(self, h: int, tokens: int, d: int, dtype: torch.dtype, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+        k = self.k
+        if k is None or k.shape[1] != h or k.shape[2] < tokens or k.shape[3] != d or k.dtype != dtype or k.device != device:
+            # Whole blocks of 256 tokens, so a turn that grows the context by a few tokens reuses it.
+            cap = -(-tokens // 256) * 256
+            self.k = torch.empty((1, h, cap, d), dtype=dtype, device=device)
+            self.v = torch.empty_like(self.k)
+        assert self.k is not None and self.v is not None
+        return self.k, self.v
 
 
 def allocate_host_pools(n_layers: int, heads: int, head_dim: int, block_size: int, capacity_tokens: int, dtype: torch.dtype = torch.bfloat16, quant: str | None = None, coherent: bool = False) -> list[torch.Tensor]:
@@ -93,17 +126,72 @@ class TieredLayer:
         """
         _lib.require_cuda(keys, values)
         _, h, length, d = keys.shape
-        n_blocks, tail = divmod(length, block_size)
+        n_blocks = length // block_size
         self._allocate(h, d, n_blocks, k_blocks, block_size, capacity_tokens, keys.device, keys.dtype, host, n_slots, quant, fetch, exact, rank_dtype)
-        src = kernels.dense_source(keys, values, block_size)
-        self._store(src, 0, n_blocks, with_store=True)
-        self.boundary_d2h_bytes = n_blocks * h * self.pair_bytes if self.host is not None else 0
+        self._open_prompt()
+        self.seal_prompt_blocks(keys, values, 0, n_blocks)
+        self.close_prompt(keys, values)
+
+    @classmethod
+    def opened(
+        cls,
+        h: int,
+        d: int,
+        prompt_tokens: int,
+        k_blocks: int,
+        block_size: int,
+        capacity_tokens: int,
+        device: torch.device,
+        dtype: torch.dtype,
+        host: torch.Tensor | None = None,
+        n_slots: int | None = None,
+        quant: str | None = None,
+        fetch: str = "zerocopy",
+        exact: bool = False,
+        rank_dtype: torch.dtype | None = torch.float32,
+    ) -> TieredLayer:
+        """A layer for a prompt of `prompt_tokens` tokens whose KV arrives in pieces: the caller seals
+        the prompt's full blocks as they become available (`seal_prompt_blocks`, in any grouping) and
+        then `close_prompt` sets the sink and the current block. The result is the constructor's."""
+        self = cls.__new__(cls)
+        self._allocate(h, d, prompt_tokens // block_size, k_blocks, block_size, capacity_tokens, torch.device(device), dtype, host, n_slots, quant, fetch, exact, rank_dtype)
+        self._open_prompt()
+        return self
+
+    def _open_prompt(self) -> None:
+        self.n_sealed, self.fill, self.length = 0, 0, 0
+        self.boundary_d2h_bytes = 0
+        self._prompt_sealed = 0  # prompt blocks [0, _prompt_sealed) are in the tier
+
+    def seal_prompt_blocks(self, keys: torch.Tensor, values: torch.Tensor, first: int, n: int) -> None:
+        """Store prompt blocks [first, first + n) of the dense KV [1, h, >= (first + n) * bs, d] into
+        the tier (host pool and/or HBM store) with their metadata: one kernel launch. Blocks must
+        arrive in order; the launch goes to the current stream."""
+        if first != self._prompt_sealed:
+            raise ValueError(f"prompt blocks must be sealed in order: expected block {self._prompt_sealed}, got {first}")
+        if n <= 0:
+            return
+        src = kernels.dense_source(keys, values, self.bs)
+        if first + n > src.n_blocks:
+            raise ValueError(f"blocks {first}..{first + n} are not all in the given KV ({src.n_blocks} full blocks)")
+        self._store(src, first, n, with_store=True)
+        self._prompt_sealed = first + n
+        if self.host is not None:
+            self.boundary_d2h_bytes += n * self.h * self.pair_bytes
+
+    def close_prompt(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Finish a prompt of L = keys.shape[2] tokens whose full blocks are sealed: the sink slot
+        takes block 0 and the current slot the L % bs tokens past the last full block."""
+        length = keys.shape[2]
+        n_blocks, tail = divmod(length, self.bs)
+        if self._prompt_sealed != n_blocks:
+            raise ValueError(f"{self._prompt_sealed} of the prompt's {n_blocks} full blocks are sealed")
         # The sink never leaves VRAM and stays exact even under an int8 tier (lazykv/tiered.py:200-202).
-        self.pool[0, :, 0] = keys[0, :, :block_size]
-        self.pool[0, :, 1] = values[0, :, :block_size]
+        self.pool[0, :, 0].copy_(keys[0, :, : self.bs])
+        self.pool[0, :, 1].copy_(values[0, :, : self.bs])
         if tail:
-            self.pool[1, :, 0, :tail] = keys[0, :, n_blocks * block_size : length]
-            self.pool[1, :, 1, :tail] = values[0, :, n_blocks * block_size : length]
+            self.pool[1, :, 0, :tail].copy_(keys[0, :, n_blocks * self.bs : length])
+            self.pool[1, :, 1, :tail].copy_(values[0, :, n_blocks * self.bs : length])
         self.n_sealed, self.fill, self.length = n_blocks, tail, length
 
     @classmethod
@@ -234,11 +322,8 @@ class TieredLayer:
 
     def load_blocks(self, pairs: torch.Tensor, first: int) -> None:
         """Store `pairs` [n, h, 2, bs, d] (GPU, model dtype) as blocks first..first+n-1 (boundary / restore)."""
-        src = kernels.pool_source(pairs.contiguous())
-        # pool_source numbers the blocks of `pairs` from 0; shift by addressing from `first` back.
-        shifted = kernels.Source(src.k - first * src.block_stride * pairs.element_size(), src.v - first * src.block_stride * pairs.element_size(),
-                                 src.block_stride, src.head_stride, src.dtype, src.deq_dtype, first + pairs.shape[0], src.owners)
-        self._store(shifted, first, pairs.shape[0], with_store=True)
+        x = pairs.contiguous()
+        self._store(_renumbered(kernels.pool_source(x), first, x.element_size()), first, pairs.shape[0], with_store=True)
         self.n_sealed = max(self.n_sealed, first + pairs.shape[0])
 
     def set_current(self, keys: torch.Tensor, values: torch.Tensor, fill: int) -> None:
@@ -254,6 +339,89 @@ class TieredLayer:
         self.pool[1, :, 1, self.fill].copy_(value[0, :, 0])
         self.fill += 1
         self.length += 1
+
+    def extend(self, keys: torch.Tensor, values: torch.Tensor, counters: TierCounters | None = None) -> None:
+        """Write a multi-token forward's KV [1, h, T, d], leaving exactly the state T calls to
+        `append` would (lazykv/tiered.py:316-332): sealing stays lazy, so a block the forward
+        fills completely stays the current block until a later token arrives.
+
+        Instead of a seal per block, at most two store launches: the current block, once it is full
+        and more tokens follow, from its slot; then every further block the forward completes
+        except the last, straight from `keys`/`values`. The last one goes to the current slot. The
+        records and metadata are per-block functions of the same bytes, so they equal the seals'.
+        """
+        _lib.require_cuda(keys, values)
+        t = keys.shape[2]
+        if keys.shape != values.shape or keys.shape[0] != 1 or keys.shape[1] != self.h or keys.shape[3] != self.d:
+            raise ValueError(f"extend takes KV [1, {self.h}, T, {self.d}], got {tuple(keys.shape)} / {tuple(values.shape)}")
+        if t == 0:
+            return
+        if self.length + t > self.cap_blocks * self.bs:
+            raise RuntimeError(f"host pool full: {self.length} + {t} tokens exceed {self.cap_blocks} blocks of {self.bs}")
+        k = keys.contiguous()
+        v = values.contiguous()
+        top = min(self.bs - self.fill, t)  # tokens that complete the current block
+        self._write_current(k, v, 0, top)
+        rest = t - top
+        if rest == 0:
+            return
+        self._seal(counters)
+        spans = -(-rest // self.bs)  # blocks the remaining tokens cover; the last stays current
+        direct = spans - 1
+        if direct:
+            first = self.n_sealed
+            src = kernels.dense_source(k[:, :, top:], v[:, :, top:], self.bs)
+            self._store(_renumbered(src, first, k.element_size()), first, direct, with_store=True)
+            self.n_sealed += direct
+            self.length += direct * self.bs
+            if counters is not None:
+                counters.seals += direct
+                counters.seal_bytes += direct * self.h * self.pair_bytes
+        self.fill = 0
+        self._write_current(k, v, top + direct * self.bs, t)
+
+    def _write_current(self, k: torch.Tensor, v: torch.Tensor, a: int, b: int) -> None:
+        """Tokens [a, b) of a forward's KV [1, h, T, d] appended to the current block's slot."""
+        n = b - a
+        if n <= 0:
+            return
+        self.pool[1, :, 0, self.fill : self.fill + n].copy_(k[0, :, a:b])
+        self.pool[1, :, 1, self.fill : self.fill + n].copy_(v[0, :, a:b])
+        self.fill += n
+        self.length += n
+
+    def dense_kv(self, keys: torch.Tensor, values: torch.Tensor, scratch: DenseScratch) -> tuple[torch.Tensor, torch.Tensor, int]:
+        """What a multi-token forward attends to (lazykv/tiered.py:334-351): this layer's whole KV --
+        the sealed blocks, the current block's `fill` tokens -- followed by `keys`/`values`
+        [1, h, T, d], as views [1, h, L + T, d] of `scratch`. Returns (keys, values, bytes read over
+        the link).
+
+        The sealed blocks are read by one store-kernel launch: in place from the host pool over the
+        link (the model-dtype pairs copied, or int8 records dequantised as the decode reads them,
+        which the reference refuses), or from the HBM store for the resident and exact tiers. Block 0
+        comes from the sink slot, which is what the decode attends (exact even under an int8 tier).
+        """
+        _lib.require_cuda(keys, values)
+        t = keys.shape[2]
+        bs, n = self.bs, self.n_sealed
+        total = n * bs + self.fill + t
+        sk, sv = scratch.take(self.h, total, self.d, self.dtype, self.pool.device)
+        moved = 0
+        if n:
+            src = self._store_src if self.store is not None else self._host_src
+            dst = kernels.dense_source(sk, sv, bs)
+            kernels.store_blocks(src, dst=dst, n_kv=self.h, head_dim=self.d, block_size=bs, first_block=0, n_blocks=n)
+            if self.store is None:
+                moved = n * self.h * self.pair_bytes
+            sk[0, :, :bs].copy_(self.pool[0, :, 0])
+            sv[0, :, :bs].copy_(self.pool[0, :, 1])
+        a = n * bs
+        if self.fill:
+            sk[0, :, a : a + self.fill].copy_(self.pool[1, :, 0, : self.fill])
+            sv[0, :, a : a + self.fill].copy_(self.pool[1, :, 1, : self.fill])
+        sk[0, :, a + self.fill : total].copy_(keys[0])
+        sv[0, :, a + self.fill : total].copy_(values[0])
+        return sk[:, :, :total], sv[:, :, :total], moved
 
     def _seal(self, counters: TierCounters | None) -> None:
         """Store the full current block as block n_sealed (lazykv/tiered.py:353-375), on the device."""
@@ -405,6 +573,7 @@ class TieredCache(Cache):
         # One index buffer and one workspace shared by every layer: layers run in order on one stream.
         self._idx = torch.empty((first.h, k_blocks), dtype=torch.int32, device=dev)
         self._ws = kernels.Workspace(dev)
+        self._dense = DenseScratch()  # multi-token forwards: the layer's whole KV, one layer at a time
         self.policy_name = "tiered_exact" if exact else ("tiered_int8" if quant else f"tiered_{fetch}")
 
     # -- transformers plumbing --------------------------------------------------------------------
@@ -414,8 +583,18 @@ class TieredCache(Cache):
         if tier is None:
             return self.full.layers[layer_idx].update(key_states, value_states)
         if key_states.shape[-2] != 1:
-            raise NotImplementedError("multi-token ingestion into the tier is outside the decode path")
+            # A multi-token forward (a user's turn) attends densely to the layer's whole KV, as the
+            # reference does (lazykv/tiered.py:649-663); the turn then enters the tier exactly as
+            # token-by-token appends would. The sealed blocks cross the link once per layer.
+            k, v, moved = tier.dense_kv(key_states, value_states, self._dense)
+            tier.extend(key_states, value_states, self.counters)
+            c = self.counters
+            c.ingest_forwards += 1
+            c.ingest_tokens += key_states.shape[-2]
+            c.ingest_h2d_bytes += moved
+            return k, v
         tier.append(key_states, value_states, self.counters)
+        # Attention never reads this: select() supplies the attention of every decode step.
         return tier.pool[1:2, :, 0], tier.pool[1:2, :, 1]
 
     def get_seq_length(self, layer_idx: int = 0) -> int:

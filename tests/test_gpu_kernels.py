@@ -555,7 +555,7 @@ def test_pinned_pool_round_trips_and_the_stream_probe_reads_it() -> None:
 
 def test_install_verifies_the_decode_kernel_and_refuses_unknown_strategies() -> None:
     """install() with the model's head counts checks decode (the HIP kernel, spare storage past the
-    live length) and chunked prefill against the float32 truth first (lazykv/attention.py:214-290);
+    live length) and chunked prefill against a float64 truth first (lazykv/attention.py:214-290);
     a strategy this build does not have is a hard error."""
     from lazykv_amd import attention
 
@@ -575,11 +575,11 @@ def test_install_verifies_the_decode_kernel_and_refuses_unknown_strategies() -> 
 def test_attention_seam_refuses_a_mask_and_reads_only_the_live_prefix() -> None:
     """After lazykv/tests/test_runtime.py:147-170: the registered attention function refuses an
     external mask (it owns causality), and `attend` over the live prefix of a preallocated store
-    whose spare rows hold large values matches the float32 truth within 1e-2 relative, for a decode
+    whose spare rows hold large values matches the float64 truth within 1e-2 relative, for a decode
     token and for a 17-token chunk. head_dim is 64, the smallest the decode kernel takes (the
     reference's test uses 16). The startup verification passes for the build's strategy and fails,
     without raising, for one the build does not have (lazykv/attention.py:248-266)."""
-    from lazykv_amd.attention import _reference, attend, lazykv_attention_forward, verify_strategies
+    from lazykv_amd.attention import _truth, attend, lazykv_attention_forward, verify_strategies
 
     q = torch.randn(1, 8, 1, 64, device="cuda", dtype=torch.float16)
     k = torch.randn(1, 2, 4, 64, device="cuda", dtype=torch.float16)
@@ -592,8 +592,8 @@ def test_attention_seam_refuses_a_mask_and_reads_only_the_live_prefix() -> None:
     k, v = store_k[:, :, :live], store_v[:, :, :live]
     for q_len in (1, 17):
         q = torch.randn(1, 8, q_len, 64, device="cuda", dtype=torch.float16, generator=gen)
-        ref = _reference(q, k, v, 64**-0.5)
-        got = attend(q, k, v, 64**-0.5).float()
+        ref = _truth(q, k, v, 64**-0.5)
+        got = attend(q, k, v, 64**-0.5).double().cpu()
         assert ((got - ref).abs().max() / ref.abs().max()).item() < 1e-2, q_len
     checks = verify_strategies(8, 2, 64, dtype=torch.float16, probe_ctx=2048, steps=4)
     assert len(checks) == 1 and checks[0].ok, checks
