@@ -136,6 +136,20 @@ int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void*
                       const lkv_kv_source* cur, const lkv_kv_source* rem, void* out, int out_dtype, float* lse,
                       void* ws, size_t ws_bytes);
 
+/* ---- allocation-free lkv_sparse_decode. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The same kernels, plan and results as lkv_sparse_decode, bit for bit; the partials go
+ * to a scratch array the library holds in each GPU's memory (LKV_STATIC_SCRATCH_BYTES per device,
+ * kept until the process ends) instead of a caller workspace. A call whose partials would exceed it
+ * (lkv_sparse_decode_workspace_bytes > LKV_STATIC_SCRATCH_BYTES) is refused with LKV_ERR_INVALID.
+ * It calls no allocating function. The stream must belong to the current device. Calls on one
+ * device share the array: calls issued in order on one stream are safe, calls that overlap on one
+ * device (other streams, other threads) race. Nothing in the array needs clearing between calls. */
+#define LKV_STATIC_SCRATCH_BYTES (16u * 1024u * 1024u)
+int lkv_sparse_decode_static(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
+                             const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride, const lkv_kv_source* sink,
+                             const lkv_kv_source* cur, const lkv_kv_source* rem, void* out, int out_dtype, float* lse);
+
 /* ---- next row: device-side hybrid residency. Replaces rung 6's host-side admit / gather
  * (lazykv/tiered.py:389-487: the least recently used slots outside the chosen set are the victims,
  * lazykv/tiered.py:397-418) with device work and no host sync. The reference itself never combined

@@ -21,6 +21,7 @@ SORTED = 1
 RANK_F32, RANK_MODEL = 0, 1
 HOST_COHERENT = 1
 SRC_HOST = 1
+STATIC_SCRATCH_BYTES = 16 * 1024 * 1024  # LKV_STATIC_SCRATCH_BYTES: the allocation-free decode's partials per device
 
 _DTYPE_CODES = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
 
@@ -86,6 +87,11 @@ SIGNATURES: dict[str, tuple] = {
         _I,
         [_U, ctypes.POINTER(DecodeDesc), _P, _I, ctypes.POINTER(KVSource), _P, _I64, ctypes.POINTER(KVSource),
          ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I, _P, _P, _SZ],
+    ),
+    "lkv_sparse_decode_static": (
+        _I,
+        [_U, ctypes.POINTER(DecodeDesc), _P, _I, ctypes.POINTER(KVSource), _P, _I64, ctypes.POINTER(KVSource),
+         ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I, _P],
     ),
     "lkv_hybrid_decode_workspace_bytes": (_SZ, [ctypes.POINTER(DecodeDesc)]),
     "lkv_hybrid_decode": (

@@ -25,6 +25,7 @@
 // launch folds each query head's partials into out and lse. (A last-arriver merge inside one
 // launch would need a device-scope release per workgroup, which writes back the whole L2; the
 // kernel boundary publishes every partial once.)
+#include <atomic>
 #include <type_traits>
 
 #include "lkv_common.h"
@@ -1424,3 +1425,47 @@ extern "C" int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, 
                             dec_bytes, slots, loc, (int64_t)d.k, &res);
 }
 
+// ---- allocation-free variant of lkv_sparse_decode ------------------------------------------------
+// The decode partials live in a file-scope device array instead of a caller workspace. In host code
+// `lkv_static_scratch` names a host-side stand-in, not device memory: its device address is looked
+// up once per device with hipGetSymbolAddress (each GPU holds its own copy of the array) and only
+// that address is handed to kernels. Calls on one device share the array, so calls that overlap on
+// one device (different streams) race; calls issued in order on one stream do not. The partials
+// are written before they are read on every call, so nothing needs clearing between calls.
+namespace {
+static __device__ __align__(256) unsigned char lkv_static_scratch[LKV_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_static_scratch[kMaxDevices];
+
+int static_scratch(void** out) {
+  int dev = 0;
+  LKV_CHECK_HIP(hipGetDevice(&dev));
+  LKV_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device %d outside the %d devices this library tracks", dev, kMaxDevices);
+  void* p = g_static_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    // With `dev` current (it is the current device): the address of that device's copy.
+    LKV_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(lkv_static_scratch)));
+    g_static_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return LKV_OK;
+}
+}  // namespace
+
+extern "C" int lkv_sparse_decode_static(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
+                                        const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride,
+                                        const lkv_kv_source* sink, const lkv_kv_source* cur, const lkv_kv_source* rem,
+                                        void* out, int out_dtype, float* lse) {
+  LKV_CHECK_ARG(desc != nullptr, "NULL argument");
+  const size_t need = lkv_sparse_decode_workspace_bytes(desc);
+  LKV_CHECK_ARG(need > 0, "bad decode shape");
+  LKV_CHECK_ARG(need <= (size_t)LKV_STATIC_SCRATCH_BYTES,
+                "this decode needs %zu bytes of partials; the allocation-free entry point holds at most %zu", need,
+                (size_t)LKV_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = static_scratch(&ws);
+  if (rc != LKV_OK) return rc;
+  return sparse_decode_impl(stream, desc, q, q_dtype, sel, idx, idx_stride, sink, cur, rem, out, out_dtype, lse, ws,
+                            (size_t)LKV_STATIC_SCRATCH_BYTES, nullptr, nullptr, 0, nullptr);
+}
