@@ -139,8 +139,10 @@ def test_prompt_longer_than_capacity_is_refused(tiny) -> None:  # noqa: ANN001
 def test_layer_major_prefill_32k_1b_shape_writes_quant_py_records() -> None:
     """The 1B-shaped prefill at its real size: 16 layers (hidden 2048, 32/8 heads, d 64), float16
     weights ~ N(0, 0.02) with unit RMSNorm gains, a 32,768-token prompt uniform over 128,256 ids,
-    every layer's KV straight into the int8 host tier. A sample of each layer's records equals
-    quant.py's pack of the chunk-major prefill's KV, and their metadata the min/max of unpack."""
+    every layer's KV straight into the int8 host tier. In every layer, every one of the 16,384
+    (block, head) records equals quant.py's pack of the chunk-major prefill's KV (the oracle's C
+    restatement, pinned to quant.py's own golden vectors), and every metadata row the min/max of
+    the keys that pack's records unpack to."""
     from transformers import LlamaConfig, LlamaForCausalLM
 
     from lazykv_amd.attention import IMPLEMENTATION_NAME, install
@@ -170,18 +172,19 @@ def test_layer_major_prefill_32k_1b_shape_writes_quant_py_records() -> None:
     want_logits = out.logits[0, -1].float()
     assert (got.last_logits - want_logits).abs().max().item() <= 4 * 2.0**-10 * max(1.0, want_logits.abs().max().item())
     assert not any(layer.is_initialized for layer in got.full.layers)
+    from oracle import quant_c
+
     nb = n // bs
-    rng = np.random.default_rng(5)
+    h = cfg.num_key_value_heads
     for i, t in got.cache.tiers.items():
         assert (t.n_sealed, t.fill) == (nb, 0)
-        blocks = rng.integers(0, nb, 64)
-        heads = rng.integers(0, cfg.num_key_value_heads, 64)
-        kb = _bits(full.layers[i].keys[0])  # [h, n, d]
-        vb = _bits(full.layers[i].values[0])
-        pairs = np.stack([np.stack([kb[h, b * bs : (b + 1) * bs], vb[h, b * bs : (b + 1) * bs]]) for b, h in zip(blocks, heads)])  # [64, 2, bs, d]
-        want = R.pack(pairs, "f16")
-        assert np.array_equal(t.host[torch.from_numpy(blocks), torch.from_numpy(heads)].numpy(), want), i
-        keys = R.to_f32(R.unpack(want, bs, d, "f16"), "f16")[:, 0]  # [64, bs, d]
-        assert np.array_equal(_bits(t.kmin[0][torch.from_numpy(heads).cuda(), torch.from_numpy(blocks).cuda()]), R.from_f32(keys.min(axis=1), "f16"))
-        assert np.array_equal(_bits(t.kmax[0][torch.from_numpy(heads).cuda(), torch.from_numpy(blocks).cuda()]), R.from_f32(keys.max(axis=1), "f16"))
+        kb = _bits(full.layers[i].keys[0, :, :n]).reshape(h, nb, bs, d)  # float16 bits
+        vb = _bits(full.layers[i].values[0, :, :n]).reshape(h, nb, bs, d)
+        pairs = np.stack([kb, vb], axis=2).transpose(1, 0, 2, 3, 4).reshape(nb * h, 2, bs, d)  # the host pool's order
+        want = quant_c.pack(pairs, "f16")  # [nb * h, P]
+        assert np.array_equal(t.host[:nb].numpy().reshape(nb * h, -1), want), f"layer {i}: records"
+        keys = R.to_f32(quant_c.unpack(want, bs, d, "f16")[:, 0], "f16").reshape(nb, h, bs, d)
+        assert np.array_equal(_bits(t.kmin[0, :, :nb]), R.from_f32(keys.min(axis=2), "f16").transpose(1, 0, 2)), f"layer {i}: kmin"
+        assert np.array_equal(_bits(t.kmax[0, :, :nb]), R.from_f32(keys.max(axis=2), "f16").transpose(1, 0, 2)), f"layer {i}: kmax"
+        print(f"layer {i}: {nb * h} records and metadata rows equal the oracle", flush=True)
     print(f"tiered prefill 32K x 16 layers: wall {got.wall_s:.3f} s, tier builds {got.boundary_s * 1e3:.2f} ms in all")
