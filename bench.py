@@ -80,6 +80,7 @@ def main() -> int:
     p.add_argument("--only", choices=["zerocopy", "hbm"], default=None, help="decode128k: one leg only")
     p.add_argument("--tier-where", choices=["hbm", "host"], default="hbm", help="int8_64k: where the int8 records live")
     p.add_argument("--eager", action="store_true", help="launch from Python instead of replaying a graph")
+    p.add_argument("--unfused", action="store_true", help="the step as two calls (lkv_bound_topk, lkv_sparse_decode) instead of one (lkv_select_decode)")
     p.add_argument("--coherent", action="store_true", help="fine-grained (device-uncached) host pools")
     p.add_argument("--drift", type=float, default=0.25, help="hybrid128k: per-step query drift (relative to the query's RMS)")
     p.add_argument("--seq", type=int, default=16, help="hybrid128k: decode steps in the sequence")
@@ -349,30 +350,50 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
     for name, k, sels, rems in legs:
         n_dense = DENSE_LAYERS if name.endswith("dense") else 0
         idx = torch.empty((H, k), dtype=torch.int32, device=dev)
-        ranks, decodes = [], []
+        ranks, decodes, checks = [], [], []
+        fused = not args.unfused and rems is None
         for li, st in enumerate(layers):
             if li < n_dense:  # dense decode: every block of the layer's KV, from HBM
                 dsrc = kernels.dense_source(st["dense"][0], st["dense"][1], BS)
                 ranks.append(None)
+                checks.append(None)
                 decodes.append(kernels.PreparedDecode(st["q"], n_kv=H, block_size=BS, scale=scale, sel=None, idx=None, sink=None, sink_block=-1, cur=None, cur_block=-1,
                                                       fill=0, out=outs[li], lse=lses[li], rem=dsrc, rem_range=(0, N), attend_selected=False, ws=ws_dec))
                 continue
-            ranks.append(kernels.PreparedBoundTopk(st["q"], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx, ws=ws_sel))
             ss = kernels.pool_source(st["slots"])
+            if fused:
+                # One call per layer (lkv_select_decode). For the per-kernel split, "rank" is what
+                # runs before the decode launch: the bound kernel, and the top-K launch when the
+                # selection is not made inside the decode launch.
+                common = dict(cand_offset=1, n_cand=n_cand, block_size=BS, scale=scale, sel=sels[li], sink=ss, sink_block=0, cur=ss, cur_block=1,
+                              fill=fill, out=outs[li], lse=lses[li], ws=ws_dec)
+                decodes.append(kernels.PreparedSelectDecode(st["q"], st["kmin"], st["kmax"], k, **common))
+                checks.append(kernels.PreparedSelectDecode(st["q"], st["kmin"], st["kmax"], k, out_idx=idx, **common))
+                if n_cand > kernels._lib.SELECT_IN_DECODE_MAX_CAND:
+                    ranks.append(kernels.PreparedBoundTopk(st["q"], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx, ws=ws_sel))
+                else:
+                    bnd = torch.empty((H, n_cand), dtype=torch.float32, device=dev)
+                    ranks.append(kernels.PreparedBoundTopk(st["q"], st["kmin"], st["kmax"], 0, cand_offset=1, n_cand=n_cand, out_bound=bnd, ws=ws_sel))
+                continue
+            ranks.append(kernels.PreparedBoundTopk(st["q"], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx, ws=ws_sel))
+            checks.append(None)
             extra = dict(rem=rems[li], rem_range=(1, n_sealed)) if rems is not None else {}
             decodes.append(kernels.PreparedDecode(st["q"], n_kv=H, block_size=BS, scale=scale, sel=sels[li], idx=idx, sink=ss, sink_block=0, cur=ss, cur_block=1,
                                                   fill=fill, out=outs[li], lse=lses[li], ws=ws_dec, **extra))
 
-        def step(ranks=ranks, decodes=decodes) -> None:  # noqa: ANN001
+        def step(ranks=ranks, decodes=decodes, fused=fused) -> None:  # noqa: ANN001
             for rk, dc in zip(ranks, decodes):
-                if rk is not None:
+                if rk is not None and not fused:
                     rk()
                 dc()
 
         # Every selecting layer's needle is selected for every KV head; outputs are finite.
         for li in range(L):
             if ranks[li] is not None:
-                ranks[li]()
+                if checks[li] is not None:
+                    checks[li]()
+                else:
+                    ranks[li]()
                 got = idx.cpu()
                 assert (got == layers[li]["needle"]).any(dim=1).all(), f"layer {li}: needle block {layers[li]['needle']} not selected"
             decodes[li]()
@@ -383,11 +404,13 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
         per = [kernel_us([ranks[li], decodes[li]], reps) for li in range(n_dense, L)]
         sel_us = statistics.mean(x[0] for x in per)
         dec_us = statistics.mean(x[1] for x in per)
+        if fused:  # the one call holds the bound (and top-K) launches too: the decode launch is the rest
+            dec_us = max(dec_us - sel_us, 1e-3)
         dense_us = statistics.mean(kernel_us([decodes[li]], reps)[0] for li in range(n_dense)) if n_dense else None
         extra = f", dense decode {dense_us:.1f} us on {n_dense} layers" if n_dense else ""
         log(f"{name}: {ms_step:.3f} ms/step = {ms_step * 1e3 / L:.1f} us/layer (bound+topk {sel_us:.1f} us, decode {dec_us:.1f} us{extra}), wall {wall:.2f}s")
         res[name] = {"k": k, "ms_step": ms_step, "us_layer": ms_step * 1e3 / L, "sel_us": sel_us, "dec_us": dec_us, "host_sel": bool(sels[0].flags), "rem": rems is not None,
-                     "dist": dist, "n_dense": n_dense, "dense_us": dense_us}
+                     "dist": dist, "n_dense": n_dense, "dense_us": dense_us, "fused": fused}
 
     # ---- probes --------------------------------------------------------------------------------
     probe = {}
@@ -437,7 +460,7 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
         dec_pcie = (b_sel if rr["host_sel"] else 0) + b_rem
         dec_hbm = B_sinkcur + B_q + B_out + (0 if rr["host_sel"] else b_sel)
         legs_out[name] = {
-            "k": rr["k"], "us_per_layer": round(rr["us_layer"], 3), "ms_per_step": round(rr["ms_step"], 4),
+            "k": rr["k"], "us_per_layer": round(rr["us_layer"], 3), "ms_per_step": round(rr["ms_step"], 4), "fused": rr["fused"],
             "step_stats": {"us_per_layer_median": round(rr["dist"]["median_ms"] * 1e3 / L, 2),
                            "us_per_layer_iqr": [round(x * 1e3 / L, 2) for x in rr["dist"]["iqr_ms"]], "steps": rr["dist"]["steps"]},
             "hbm_bytes_per_layer": hb, "pcie_bytes_per_layer": pb,
@@ -481,6 +504,11 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             "rank_note": "the reference's tier ranks on the bound rounded to the model dtype (top_blocks dtype=None); this step ranks on the float32 bound, "
                          "so its selected sets equal the reference's except in near-tie cells (|b_K - b_K+1| <= 1e-5 max(1, |b_K|))",
             "dense_layers": 0, "launch": "eager" if args.eager else "hip_graph",
+            "launches_per_layer": 3 if (m["fused"] and n_cand <= kernels._lib.SELECT_IN_DECODE_MAX_CAND) else 4,
+            "step_kernels": ("one lkv_select_decode call: bound_kernel, sparse_decode_kernel choosing the top K itself, decode_merge_kernel"
+                             if (m["fused"] and n_cand <= kernels._lib.SELECT_IN_DECODE_MAX_CAND) else
+                             ("one lkv_select_decode call: " if m["fused"] else "lkv_bound_topk + lkv_sparse_decode: ")
+                             + "bound_kernel, select_kernel, sparse_decode_kernel, decode_merge_kernel"),
             "host_memory": "fine-grained" if args.coherent else "coarse-grained",
         },
         "host_syncs_per_layer": 0,
@@ -490,7 +518,9 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
     traffic = pmc_traffic() if kind == "host" else {}
     if m["sparse_decode_pcie_bytes"]:
         gbps = m["sparse_decode_pcie_gbps"]
-        out["roofline"] = {"bound": "pcie", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, host reads over PCIe", "achieved": gbps,
+        kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and n_cand <= kernels._lib.SELECT_IN_DECODE_MAX_CAND)
+                 else "sparse_decode_kernel + decode_merge_kernel")
+        out["roofline"] = {"bound": "pcie", "kernel": f"{kname}, host reads over PCIe", "achieved": gbps,
                            "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get("zerocopy/sparse_decode_kernel"),
                            "algorithmic_bytes": m["sparse_decode_pcie_bytes"], "kernel_us": m["sparse_decode_us"]}
         if probe.get("dma_h2d_gbps"):
@@ -502,7 +532,9 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             out["roofline"]["traffic_run"] = pmc_run("zerocopy")
     else:
         gbps = m["sparse_decode_hbm_gbps"]
-        out["roofline"] = {"bound": "hbm", "kernel": "lkv_sparse_decode: sparse_decode_kernel + decode_merge_kernel, HBM", "achieved": gbps,
+        kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and n_cand <= kernels._lib.SELECT_IN_DECODE_MAX_CAND)
+                 else "sparse_decode_kernel + decode_merge_kernel")
+        out["roofline"] = {"bound": "hbm", "kernel": f"{kname}, HBM", "achieved": gbps,
                            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get("hbm/sparse_decode_kernel"),
                            "algorithmic_bytes": m["sparse_decode_hbm_bytes"], "kernel_us": m["sparse_decode_us"]}
     out["byte_roofline"] = {"hbm_bytes_per_layer": m["hbm_bytes_per_layer"], "pcie_bytes_per_layer": m["pcie_bytes_per_layer"],
@@ -530,11 +562,15 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
         # parity figure beside the timing (the timed steps write the model dtype).
         name0, k0, sels0, rems0 = legs[0]
         st0 = layers[0]
-        idx0 = kernels.bound_topk(st0["q"], st0["kmin"], st0["kmax"], k0, cand_offset=1, n_cand=n_cand)
         ss0 = kernels.pool_source(st0["slots"])
-        extra0 = dict(rem=rems0[0], rem_range=(1, n_sealed)) if rems0 is not None else {}
-        f32 = kernels.sparse_decode(st0["q"], n_kv=H, block_size=BS, scale=scale, sel=sels0[0], idx=idx0, sink=ss0, sink_block=0, cur=ss0, cur_block=1,
-                                    fill=fill, out_dtype=torch.float32, **extra0)
+        if res[name0]["fused"]:
+            f32 = kernels.select_decode(st0["q"], st0["kmin"], st0["kmax"], k0, cand_offset=1, n_cand=n_cand, block_size=BS, scale=scale, sel=sels0[0],
+                                        sink=ss0, sink_block=0, cur=ss0, cur_block=1, fill=fill, out_dtype=torch.float32)
+        else:
+            idx0 = kernels.bound_topk(st0["q"], st0["kmin"], st0["kmax"], k0, cand_offset=1, n_cand=n_cand)
+            extra0 = dict(rem=rems0[0], rem_range=(1, n_sealed)) if rems0 is not None else {}
+            f32 = kernels.sparse_decode(st0["q"], n_kv=H, block_size=BS, scale=scale, sel=sels0[0], idx=idx0, sink=ss0, sink_block=0, cur=ss0, cur_block=1,
+                                        fill=fill, out_dtype=torch.float32, **extra0)
         torch.cuda.synchronize()
         out["cpu_baseline"] = cpu_baseline_decode(kind, layers, ks[0], n_sealed, fill, scale, args.cpu_seconds, outs, last, (name0, k0, f32))
     return out

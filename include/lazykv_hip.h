@@ -10,9 +10,9 @@
  *    PCIe in place.
  *  - `stream` is a hipStream_t passed as an integer (0 = the null stream). Work is enqueued only:
  *    no entry point synchronises the stream, and none allocates device memory. Scratch space is
- *    the caller's `ws` buffer, sized by the matching *_workspace_bytes function; it needs no
- *    initialisation and can be reused by calls issued in order on one stream. Calls that overlap
- *    on different streams need distinct workspaces.
+ *    the caller's `ws` buffer, sized by the matching *_workspace_bytes function and 16-byte
+ *    aligned; it needs no initialisation and can be reused by calls issued in order on one
+ *    stream. Calls that overlap on different streams need distinct workspaces.
  *  - Return value: LKV_OK (0) or a negative LKV_ERR_*; shapes and arguments are validated before
  *    any launch. lkv_last_error() returns a message for the calling thread's last failure.
  *  - Dtype codes: LKV_F16, LKV_BF16, LKV_F32 for model-dtype tensors; LKV_INT8_RECORD for the
@@ -135,6 +135,22 @@ int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void*
                       const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride, const lkv_kv_source* sink,
                       const lkv_kv_source* cur, const lkv_kv_source* rem, void* out, int out_dtype, float* lse,
                       void* ws, size_t ws_bytes);
+
+/* ---- a1 + a2 + a5 + a6: one selecting layer's decode step
+ * (lazykv/tiered.py:383-387 rank + :489-511 gather_zerocopy + lazykv/attention.py:97-136 attend;
+ * the top_blocks rule of lazykv/selection.py:56-62). The bound kernel scores candidates
+ * cand_offset .. cand_offset+n_cand-1 of every KV head into the workspace; each head's top desc->k
+ * -- the same set as lkv_bound_topk, ties to the lower id -- is then chosen inside the decode
+ * launch (up to 4,096 candidates per head: two launches for bound, top-K and attention, plus the
+ * merge) or by its own launch (beyond), and the sink, the selected blocks (from `sel`) and the
+ * current block are attended as lkv_sparse_decode does. The result equals lkv_bound_topk followed
+ * by lkv_sparse_decode, bit for bit. out_idx, if not NULL, receives the selected ids in ascending
+ * order (idx_stride apart per head). No remainder; up to 262,144 candidates per head. */
+size_t lkv_select_decode_workspace_bytes(const lkv_decode_desc* desc, int n_cand);
+int lkv_select_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype, const void* kmin,
+                      const void* kmax, int meta_dtype, int64_t meta_head_stride, int cand_offset, int n_cand, int rank_mode,
+                      const lkv_kv_source* sel, const lkv_kv_source* sink, const lkv_kv_source* cur, void* out, int out_dtype,
+                      float* lse, int32_t* out_idx, int64_t idx_stride, void* ws, size_t ws_bytes);
 
 /* ---- allocation-free lkv_sparse_decode. No counterpart in the reference: for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid

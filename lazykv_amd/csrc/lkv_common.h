@@ -46,6 +46,18 @@ void lkv_clear_error();
 
 static inline size_t lkv_align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// The bound kernel alone (lkv_select.hip), for entry points that validate their own arguments and
+// select inside a later launch: float32 bounds of candidates [cand_offset, cand_offset + n_cand) of
+// every KV head to bounds + h * bstride.
+int lkv_launch_bounds(hipStream_t stream, const void* q, int q_dtype, const void* kmin, const void* kmax, int meta_dtype,
+                      int64_t meta_head_stride, int n_kv, int g, int head_dim, int cand_offset, int n_cand, int rank_mode,
+                      float* bounds, int64_t bstride);
+// The top-k launch alone (lkv_select.hip): ascending ids (cand_offset included) of each head's k
+// highest bounds to out_idx + h * idx_stride. n_cand up to lkv_select_max_candidates().
+int lkv_launch_select(hipStream_t stream, const float* bounds, int64_t bstride, int n_kv, int n_cand, int k, int cand_offset,
+                      int32_t* out_idx, int64_t idx_stride);
+int lkv_select_max_candidates();
+
 static inline bool lkv_is_model_dtype(int dt) { return dt == LKV_F16 || dt == LKV_BF16 || dt == LKV_F32; }
 
 static inline int lkv_dtype_size(int dt) { return dt == LKV_F32 ? 4 : (dt == LKV_INT8_RECORD ? 1 : 2); }

@@ -28,6 +28,7 @@
 #include <atomic>
 #include <type_traits>
 
+#include "lkv_blockselect.h"
 #include "lkv_common.h"
 
 namespace {
@@ -85,6 +86,15 @@ struct DecodeArgs {
   int64_t loc_stride;
   Src slots;
   int nt;  // workgroup size the plan chose (kThreads or kThreadsHbm)
+  // Fused selection (SEL instances): the float32 bounds of candidates cand_offset .. cand_offset +
+  // n_cand - 1 of head h at bounds + h * bound_stride (rows padded to a multiple of 4 floats when
+  // bounds_aligned); the launch selects the top k itself instead of reading idx. idx_out, if set,
+  // receives the selected ids in ascending order.
+  const float* bounds;
+  int64_t bound_stride;
+  int n_cand, cand_offset, bounds_aligned;
+  int32_t* idx_out;
+  int64_t idx_out_stride;
 };
 
 constexpr int32_t kLocMiss = 0x40000000;
@@ -588,10 +598,10 @@ __device__ __forceinline__ void consume_mf(const typename Mfma<MT>::V8 (&qb)[D /
 
 // Item j0 + u * NW (u < NP) of a segment-A run [.., last): the sink is item 0 when present, the
 // current block the last item (n_a - 1) when present, and the items between are the selected ids in
-// idx order. An item past the run gets block -1 (skipped). Wave-uniform; the ids are read into
-// scalar registers.
+// idx order (selected position p at idx_h[p - base]). An item past the run gets block -1 (skipped).
+// Wave-uniform; the ids are read into scalar registers.
 template <int NP, int NW>
-__device__ __forceinline__ void segment_items(const DecodeArgs& a, const int32_t* idx_h, int j0, int last, Src (&s)[NP],
+__device__ __forceinline__ void segment_items(const DecodeArgs& a, const int32_t* idx_h, int base, int j0, int last, Src (&s)[NP],
                                               int (&blk)[NP], int (&lim)[NP]) {
   const int has_sink = a.sink_block >= 0;
 #pragma unroll
@@ -609,7 +619,7 @@ __device__ __forceinline__ void segment_items(const DecodeArgs& a, const int32_t
         blk[u] = a.cur_block;
         lim[u] = a.fill;
       } else {
-        blk[u] = __builtin_amdgcn_readfirstlane(idx_h[it - has_sink]);
+        blk[u] = __builtin_amdgcn_readfirstlane(idx_h[it - has_sink - base]);
       }
     }
   }
@@ -695,8 +705,15 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
   }
 }
 
+// Candidates a fused-selection workgroup holds (KPT keys per thread): 4,096 per KV head, a
+// 65,536-token context at 16-token blocks. Longer contexts select in their own launch.
+constexpr int kSelCap = 4096;
+template <int NT>
+constexpr int kSelKpt = kSelCap / NT;
+
 // MF: Q.K on the matrix cores (model-dtype instances whose query has the model dtype).
-template <int D, int MT, int G, int NT, bool I8, bool MF = false>
+// SEL: the launch selects each head's top k from its bounds itself (segment A only).
+template <int D, int MT, int G, int NT, bool I8, bool MF = false, bool SEL = false>
 __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   using L = Lanes<D>;
   constexpr int NW = NT / 64;
@@ -712,7 +729,41 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   __shared__ uint32_t s_excl[64];  // segment B: bitmap of excluded blocks in this run
   static_assert(!MF || (!I8 && MT != LKV_F32), "the matrix-core path reads model-dtype pairs");
   __shared__ float s_pb[MF ? NW : 1][MF ? kMfBroadcast<G, kMfMaxPairs> : 1];
+  using SelLds = typename std::conditional<SEL, lkv::SelectLds<NT, kSelKpt<NT>>, char>::type;
+  __shared__ SelLds s_sel;
   using V8 = typename Mfma<MT == LKV_F32 ? LKV_F16 : MT>::V8;
+
+  // ---- fused selection: this head's top k, and the ids of this workgroup's run -----------------
+  // The run's selected ids go to LDS (over the histogram, free once the selection is done), as
+  // positions [sel_base, sel_base + run) of the ascending selected list.
+  const int32_t* idx_h;
+  int sel_base = 0;
+  if constexpr (!SEL) {
+    idx_h = a.idx + (int64_t)h * a.idx_stride;
+  } else {
+    const lkv::SelectPick pk = lkv::block_top_k<NT, kSelKpt<NT>>(a.bounds + (int64_t)h * a.bound_stride, a.bounds_aligned != 0, a.n_cand, a.k, s_sel);
+    const int has_sink = a.sink_block >= 0;
+    const int first = split * a.per_a;
+    const int last = min(a.n_a, first + a.per_a);
+    const int js = max(first, has_sink) - has_sink;
+    const int je = min(last, has_sink + a.k) - has_sink;
+    int32_t* ids = (int32_t*)s_sel.hist;
+    int32_t* out_h = (a.idx_out != nullptr && split == 0) ? a.idx_out + (int64_t)h * a.idx_out_stride : nullptr;
+    int pos = pk.pos;
+#pragma unroll
+    for (int u = 0; u < kSelKpt<NT>; ++u) {
+      if ((pk.take >> u) & 1u) {
+        const int32_t id = pk.i0 + u + a.cand_offset;
+        if (pos >= js && pos < je) ids[pos - js] = id;
+        if (out_h != nullptr) out_h[pos] = id;
+        ++pos;
+      }
+    }
+    __syncthreads();
+    idx_h = ids;
+    sel_base = js;
+  }
+
   V8 qb[D / 32];
   if constexpr (MF) load_query_mf<D, MT, G>(a.q, h, lane, qb);
   float* sp = s_pb[MF ? wave : 0];
@@ -747,11 +798,10 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       // round.
       constexpr int kMfItems = kMfMaxPairs;
       const int wv = __builtin_amdgcn_readfirstlane(wave);
-      const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
       for (int j0 = first + wv; j0 < last; j0 += kMfItems * NW) {
         Src is[kMfItems];
         int ib[kMfItems], il[kMfItems];
-        segment_items<kMfItems, NW>(a, idx_h, j0, last, is, ib, il);
+        segment_items<kMfItems, NW>(a, idx_h, sel_base, j0, last, is, ib, il);
         process_items_mf<D, MT, G, kMfItems>(a, is, ib, il, h, qb, lane, r, c, sp, st);
       }
     } else {
@@ -761,16 +811,18 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       // Selected items of this run: idx positions [js, je), two per wave per round.
       const int js = max(first, has_sink) - has_sink;
       const int je = min(last, has_sink + n_sel) - has_sink;
-      const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
       // The hybrid branch is compiled only into the 4-wave general instance, which every hybrid
       // launch takes. The 8-wave vector-path instances keep two selected pairs in flight per wave:
       // with about two items per wave in the HBM plan, both loads are issued before either is
       // consumed (int8 records in HBM 24.4 -> 23.5 us, identical results). Float32 pools keep one
       // (two would spill).
-      constexpr bool HYB = I8 && NT == kThreads;
-      constexpr int NPA = (HYB || MT == LKV_F32) ? 1 : 2;
+      // A fused-selection instance keeps the pairing of the instance it stands in for, so that both
+      // fold each wave's chunks in the same order (with two pairs in flight a wave interleaves their
+      // 16-row chunks).
+      constexpr bool HYB = I8 && NT == kThreads && !SEL;
+      constexpr int NPA = ((I8 && NT == kThreads) || MT == LKV_F32) ? 1 : 2;
       for (int j = js + wave; j < je; j += NPA * NW) {
-        const int b0 = idx_h[j];
+        const int b0 = idx_h[j - sel_base];
         if constexpr (HYB) {
           if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
             const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
@@ -786,18 +838,17 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
             continue;
           }
         }
-        const int b1 = (NPA == 2 && j + NW < je) ? idx_h[j + NW] : -1;
+        const int b1 = (NPA == 2 && j + NW < je) ? idx_h[j + NW - sel_base] : -1;
         attend_two<D, MT, G, I8, NPA>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
       }
     }
-  } else {
+  } else if constexpr (!SEL) {
     // Segment B: remainder blocks of this run that idx does not name.
     const int sb = split - a.splits_a;
     const int lo = a.rem_first + sb * a.per_b;
     const int hi = min(a.rem_last, lo + a.per_b);
     for (int i = threadIdx.x; i < 64; i += NT) s_excl[i] = 0;
     __syncthreads();
-    const int32_t* idx_h = a.idx + (int64_t)h * a.idx_stride;
     // Eight index loads in flight per thread per round.
     for (int i0 = threadIdx.x; i0 < a.k; i0 += 8 * NT) {
       int bv[8];
@@ -865,19 +916,19 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][j]);
-    float O = 0.0f, L = 0.0f;
+    float O = 0.0f, Lsum = 0.0f;
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
         const float wt = exp2f(s_m[w][j] - M);
         O += s_o[w][j][dd] * wt;
-        L += s_l[w][j] * wt;
+        Lsum += s_l[w][j] * wt;
       }
     }
     po[t] = O;
     if (dd == 0) {
       pml[2 * j] = M;
-      pml[2 * j + 1] = L;
+      pml[2 * j + 1] = Lsum;
     }
   }
 }
@@ -1045,41 +1096,69 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
   return p;
 }
 
+// The kernel instance a launch takes. HBM plans (a.nt == kThreadsHbm, G <= 4) run 8-wave
+// workgroups: matrix-core scoring when the query has the model dtype and 16-byte aligned rows, the
+// vector path otherwise, int8-capable when a source is int8 records (except D 128 with G 4, which
+// spills there and takes the 4-wave instance over the same plan). Host plans, hybrid launches and
+// groups of 8 take the 4-wave general instance. A fused-selection launch has no 8-wave vector
+// instance and takes the general one instead.
+enum class Inst { kGeneral, kVector8, kInt8x8, kMatrix8 };
+
 template <int D, int MT, int G>
-int launch(hipStream_t stream, DecodeArgs& a) {
-  const int S = a.splits_a + a.splits_b;
-  // Instances with int8 code for int8 sources; hybrid launches take the 4-wave one (the only one
-  // with the hybrid branch).
+Inst pick_instance(const DecodeArgs& a, bool sel) {
   const bool i8 = a.sel.dtype == LKV_INT8_RECORD || a.rem.dtype == LKV_INT8_RECORD || a.sink.dtype == LKV_INT8_RECORD ||
                   a.cur.dtype == LKV_INT8_RECORD || a.loc != nullptr;
-  bool launched = false;
-  if constexpr (G <= 4) {
-    if (a.nt == kThreadsHbm) {
-      // The int8-capable 512-thread kernel spills at D = 128, G = 4; such a launch takes the
-      // 256-thread kernel over the same plan (its waves stride the same runs of items).
-      if (!i8) {
-        // Q.K on the matrix cores when the query has the model dtype and 16-byte aligned rows.
-        bool mf = false;
-        if constexpr (MT != LKV_F32) mf = a.q_dtype == MT && ((uintptr_t)a.q & 15u) == 0;
-        if (mf) {
-          if constexpr (MT != LKV_F32)
-            hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false, true>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
-        } else {
-          hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
-        }
-        launched = true;
-      } else if (a.loc != nullptr) {
-        // hybrid: the 4-wave general instance below
-      } else if constexpr (!(D == 128 && G == 4)) {
-        hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, true>), dim3(S * a.n_kv), dim3(kThreadsHbm), 0, stream, a);
-        launched = true;
-      }
+  if (G > 4 || a.nt != kThreadsHbm || a.loc != nullptr) return Inst::kGeneral;
+  if (!i8) {
+    const bool mf = MT != LKV_F32 && a.q_dtype == MT && ((uintptr_t)a.q & 15u) == 0;
+    if (mf) return Inst::kMatrix8;
+    return sel ? Inst::kGeneral : Inst::kVector8;
+  }
+  return (D == 128 && G == 4) ? Inst::kGeneral : Inst::kInt8x8;
+}
+
+template <int D, int MT, int G, bool SEL>
+int launch_inst(hipStream_t stream, DecodeArgs& a, Inst inst) {
+  const dim3 grid((a.splits_a + a.splits_b) * a.n_kv);
+  bool done = false;
+  if constexpr (MT != LKV_F32 && G <= 4) {
+    if (inst == Inst::kMatrix8) {
+      hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false, true, SEL>), grid, dim3(kThreadsHbm), 0, stream, a);
+      done = true;
     }
   }
-  if (!launched) {
-    hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreads, true>), dim3(S * a.n_kv), dim3(kThreads), 0, stream, a);
+  if constexpr (G <= 4 && !SEL) {
+    if (inst == Inst::kVector8) {
+      hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false>), grid, dim3(kThreadsHbm), 0, stream, a);
+      done = true;
+    }
   }
+  if constexpr (G <= 4 && !(D == 128 && G == 4)) {
+    if (inst == Inst::kInt8x8) {
+      hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, true, false, SEL>), grid, dim3(kThreadsHbm), 0, stream, a);
+      done = true;
+    }
+  }
+  if (!done) hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreads, true, false, SEL>), grid, dim3(kThreads), 0, stream, a);
   LKV_CHECK_LAUNCH("sparse_decode");
+  return LKV_OK;
+}
+
+// The decode launch, then the launch that folds each query head's partials into its output and LSE.
+// (Folding them in the decode launch -- its last workgroup per head reading the others' partials
+// through device-scope stores and an arrival counter -- was measured about 2 us per layer slower:
+// each device-scope access pays a memory round trip, three in a row, where the second launch pays
+// one, and its launch overlaps the decode's drain.)
+template <int D, int MT, int G>
+int launch(hipStream_t stream, DecodeArgs& a) {
+  const bool sel = a.bounds != nullptr;
+  const int S = a.splits_a + a.splits_b;
+  Inst inst = pick_instance<D, MT, G>(a, sel);
+  if ((inst == Inst::kMatrix8 && (MT == LKV_F32 || G > 4)) || (inst == Inst::kInt8x8 && (G > 4 || (D == 128 && G == 4))) ||
+      (inst == Inst::kVector8 && (G > 4 || sel)))
+    inst = Inst::kGeneral;  // no such instance (pick_instance never asks for one)
+  const int rc = sel ? launch_inst<D, MT, G, true>(stream, a, inst) : launch_inst<D, MT, G, false>(stream, a, inst);
+  if (rc != LKV_OK) return rc;
   hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(512), 0, stream, a.part_ml, a.part_o, S,
                      a.out, a.out_dtype, a.lse);
   LKV_CHECK_LAUNCH("decode_merge");
@@ -1263,11 +1342,33 @@ struct ResidencyArgs {
   int64_t slot_block_stride;
 };
 
+// A fused selection: the bound kernel scores every candidate into `bounds`, then the decode launch
+// picks each head's top k from them itself.
+struct FusedSelect {
+  const void* kmin;
+  const void* kmax;
+  int meta_dtype;
+  int64_t meta_head_stride;
+  int rank_mode;
+  float* bounds;
+  int64_t stride;  // floats between heads' rows
+  int n_cand, cand_offset;
+  bool aligned;  // rows padded to a multiple of 4 floats, 16-byte aligned
+  int32_t* idx_out;
+  int64_t idx_out_stride;
+  // false: the top k is chosen by its own launch into `ids` (idx_out, or workspace), and the decode
+  // launch reads them, as after lkv_bound_topk
+  bool in_decode;
+  int32_t* ids;
+  int64_t ids_stride;
+};
+
 static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
                               const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride,
                               const lkv_kv_source* sink, const lkv_kv_source* cur, const lkv_kv_source* rem,
                               void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes,
-                              const lkv_kv_source* slots, int32_t* loc, int64_t loc_stride, const ResidencyArgs* res) {
+                              const lkv_kv_source* slots, int32_t* loc, int64_t loc_stride, const ResidencyArgs* res,
+                              const FusedSelect* fsel = nullptr) {
   LKV_CHECK_ARG(desc != nullptr && q != nullptr && out != nullptr && lse != nullptr, "NULL argument");
   const lkv_decode_desc& d = *desc;
   LKV_CHECK_ARG(d.n_kv > 0 && d.n_q > 0 && d.n_q % d.n_kv == 0, "n_q=%d must be a positive multiple of n_kv=%d",
@@ -1280,7 +1381,7 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
   LKV_CHECK_ARG(d.rem_last >= d.rem_first && d.rem_first >= 0, "bad remainder range");
   const bool has_rem = d.rem_last > d.rem_first;
   const bool attend_sel = d.attend_selected && d.k > 0;
-  LKV_CHECK_ARG(d.k == 0 || (idx != nullptr && idx_stride >= d.k), "idx missing or idx_stride < k");
+  LKV_CHECK_ARG(d.k == 0 || fsel != nullptr || (idx != nullptr && idx_stride >= d.k), "idx missing or idx_stride < k");
   // The model dtype is that of the first model-dtype source present.
   int mt = -1;
   for (const lkv_kv_source* s : {sink, cur, sel, rem}) {
@@ -1365,8 +1466,38 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
   a.loc = loc;
   a.loc_stride = loc_stride;
   if (slots) a.slots = to_src(slots);
+  const bool select_in_decode = fsel != nullptr && fsel->in_decode;
+  if (fsel != nullptr) {
+    LKV_CHECK_ARG(attend_sel && !has_rem && res == nullptr, "a fused selection attends a selection, with no remainder and no residency");
+    LKV_CHECK_ARG(fsel->bounds != nullptr && fsel->n_cand > 0 && d.k <= fsel->n_cand, "selection of k=%d from %d candidates", d.k,
+                  fsel->n_cand);
+    LKV_CHECK_ARG(!select_in_decode || (fsel->n_cand <= kSelCap && p.per_a <= lkv::kSelBins),
+                  "a selection inside the decode launch takes at most %d candidates and %d items per workgroup", kSelCap, lkv::kSelBins);
+    LKV_CHECK_ARG(select_in_decode || fsel->ids != nullptr, "no room for the selected ids");
+  }
+  if (select_in_decode) {
+    a.bounds = fsel->bounds;
+    a.bound_stride = fsel->stride;
+    a.n_cand = fsel->n_cand;
+    a.cand_offset = fsel->cand_offset;
+    a.bounds_aligned = fsel->aligned ? 1 : 0;
+    a.idx_out = fsel->idx_out;
+    a.idx_out_stride = fsel->idx_out_stride;
+  }
 
   hipStream_t s = (hipStream_t)stream;
+  if (fsel != nullptr) {  // every argument is checked: score the candidates, then select and attend
+    int rc = lkv_launch_bounds(s, q, q_dtype, fsel->kmin, fsel->kmax, fsel->meta_dtype, fsel->meta_head_stride, d.n_kv,
+                               d.n_q / d.n_kv, d.head_dim, fsel->cand_offset, fsel->n_cand, fsel->rank_mode, fsel->bounds,
+                               fsel->stride);
+    if (rc == LKV_OK && !select_in_decode) {
+      rc = lkv_launch_select(s, fsel->bounds, fsel->stride, d.n_kv, fsel->n_cand, d.k, fsel->cand_offset, fsel->ids,
+                             fsel->ids_stride);
+      a.idx = fsel->ids;
+      a.idx_stride = fsel->ids_stride;
+    }
+    if (rc != LKV_OK) return rc;
+  }
   if (res) {  // every argument is checked: update the residency tables, then attend
     hipLaunchKernelGGL(residency_kernel, dim3(d.n_kv), dim3(kResThreads), 0, s, idx, idx_stride, d.k, res->block_slot,
                        res->block_slot_stride, sel->n_blocks, res->slot_block, res->slot_block_stride, loc, loc_stride);
@@ -1468,4 +1599,70 @@ extern "C" int lkv_sparse_decode_static(uintptr_t stream, const lkv_decode_desc*
   if (rc != LKV_OK) return rc;
   return sparse_decode_impl(stream, desc, q, q_dtype, sel, idx, idx_stride, sink, cur, rem, out, out_dtype, lse, ws,
                             (size_t)LKV_STATIC_SCRATCH_BYTES, nullptr, nullptr, 0, nullptr);
+}
+
+// ---- a1 + a2 + a5 + a6: one selecting layer's decode step ---------------------------------------
+// Where the top k is chosen. Inside the decode launch it saves the selection's own launch, but every
+// decode workgroup then waits for its own pass over all of the head's bounds; measured on MI355X,
+// the in-launch selection wins at 2,046 and 4,094 candidates per head (1.5 and 1.9 us per layer at
+// the 32K- and 64K-token 1B shapes) and loses at 8,190 (1.7 us at the 128K-token 8B shape), where
+// the one-workgroup-per-head selection launch is quicker. Up to kFuseMaxCand candidates it selects
+// in the decode launch, beyond it in its own; the results are the same bits either way.
+constexpr int kFuseMaxCand = kSelCap;
+
+extern "C" size_t lkv_select_decode_workspace_bytes(const lkv_decode_desc* desc, int n_cand) {
+  const size_t base = lkv_sparse_decode_workspace_bytes(desc);
+  if (base == 0 || n_cand <= 0) return 0;
+  // partials | bounds | the selected ids when they are chosen in their own launch
+  return base + lkv_align_up((size_t)desc->n_kv * lkv_align_up((size_t)n_cand, 4) * 4, 256) +
+         lkv_align_up((size_t)desc->n_kv * (size_t)(desc->k > 0 ? desc->k : 0) * 4, 256);
+}
+
+extern "C" int lkv_select_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype, const void* kmin,
+                                 const void* kmax, int meta_dtype, int64_t meta_head_stride, int cand_offset, int n_cand,
+                                 int rank_mode, const lkv_kv_source* sel, const lkv_kv_source* sink, const lkv_kv_source* cur,
+                                 void* out, int out_dtype, float* lse, int32_t* out_idx, int64_t idx_stride, void* ws,
+                                 size_t ws_bytes) {
+  LKV_CHECK_ARG(desc != nullptr && q != nullptr && kmin != nullptr && kmax != nullptr, "NULL argument");
+  const lkv_decode_desc& d = *desc;
+  LKV_CHECK_ARG(d.head_dim == 64 || d.head_dim == 128, "head_dim %d unsupported (64 or 128)", d.head_dim);
+  LKV_CHECK_ARG(d.n_kv > 0 && d.n_q > 0 && d.n_q % d.n_kv == 0, "n_q=%d must be a positive multiple of n_kv=%d", d.n_q, d.n_kv);
+  const int g = d.n_q / d.n_kv;
+  LKV_CHECK_ARG(g == 1 || g == 2 || g == 4 || g == 8, "unsupported GQA group size %d (1, 2, 4 or 8)", g);
+  LKV_CHECK_ARG(meta_dtype == LKV_F16 || meta_dtype == LKV_BF16, "metadata dtype must be f16 or bf16");
+  LKV_CHECK_ARG(lkv_is_model_dtype(q_dtype), "bad query dtype");
+  LKV_CHECK_ARG(rank_mode == LKV_RANK_F32 || rank_mode == LKV_RANK_MODEL, "bad rank mode");
+  LKV_CHECK_ARG(cand_offset >= 0 && n_cand > 0, "bad candidate range");
+  LKV_CHECK_ARG(n_cand <= lkv_select_max_candidates(), "%d candidate blocks exceed the per-head select limit %d", n_cand,
+                lkv_select_max_candidates());
+  LKV_CHECK_ARG(d.k > 0 && d.k <= n_cand && d.attend_selected, "selected k=%d must be in 1..n_cand=%d, attended", d.k, n_cand);
+  LKV_CHECK_ARG(meta_head_stride >= (int64_t)(cand_offset + n_cand) * d.head_dim, "metadata head stride too small");
+  LKV_CHECK_ARG(out_idx == nullptr || idx_stride >= d.k, "idx_stride < k");
+  const size_t dec = lkv_sparse_decode_workspace_bytes(desc);
+  const size_t need = lkv_select_decode_workspace_bytes(desc, n_cand);
+  LKV_CHECK_ARG(ws != nullptr && ws_bytes >= need, "workspace of %zu bytes needed, got %zu", need, ws_bytes);
+  LKV_CHECK_ARG(((uintptr_t)ws & 15) == 0, "workspace must be 16-byte aligned");
+  FusedSelect fs{};
+  fs.kmin = kmin;
+  fs.kmax = kmax;
+  fs.meta_dtype = meta_dtype;
+  fs.meta_head_stride = meta_head_stride;
+  fs.rank_mode = rank_mode;
+  fs.bounds = (float*)((char*)ws + dec);  // after the decode's partials (dec is a multiple of 256)
+  fs.stride = (int64_t)lkv_align_up((size_t)n_cand, 4);
+  fs.n_cand = n_cand;
+  fs.cand_offset = cand_offset;
+  fs.aligned = true;
+  fs.idx_out = out_idx;
+  fs.idx_out_stride = idx_stride;
+  fs.in_decode = n_cand <= kFuseMaxCand;
+  if (out_idx != nullptr) {
+    fs.ids = out_idx;
+    fs.ids_stride = idx_stride;
+  } else {
+    fs.ids = (int32_t*)((char*)fs.bounds + lkv_align_up((size_t)d.n_kv * (size_t)fs.stride * 4, 256));
+    fs.ids_stride = d.k;
+  }
+  return sparse_decode_impl(stream, desc, q, q_dtype, sel, nullptr, 0, sink, cur, nullptr, out, out_dtype, lse, ws, dec, nullptr,
+                            nullptr, 0, nullptr, &fs);
 }

@@ -630,6 +630,36 @@ extern "C" size_t lkv_bound_topk_workspace_bytes(int n_kv, int n_cand, int k) {
   return lkv_align_up((size_t)n_kv * lkv_align_up((size_t)n_cand, 4) * 4, 256);
 }
 
+int lkv_launch_bounds(hipStream_t s, const void* q, int q_dtype, const void* kmin, const void* kmax, int meta_dtype,
+                      int64_t meta_head_stride, int n_kv, int g, int head_dim, int cand_offset, int n_cand, int rank_mode,
+                      float* bounds, int64_t bstride) {
+  if (head_dim == 128) {
+    return meta_dtype == LKV_BF16 ? dispatch_g<128, LKV_BF16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv, cand_offset,
+                                                               n_cand, rank_mode, bounds, bstride)
+                                  : dispatch_g<128, LKV_F16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv, cand_offset,
+                                                              n_cand, rank_mode, bounds, bstride);
+  }
+  return meta_dtype == LKV_BF16 ? dispatch_g<64, LKV_BF16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv, cand_offset,
+                                                            n_cand, rank_mode, bounds, bstride)
+                                : dispatch_g<64, LKV_F16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv, cand_offset, n_cand,
+                                                           rank_mode, bounds, bstride);
+}
+
+int lkv_select_max_candidates() { return kMaxStreamCand; }
+
+int lkv_launch_select(hipStream_t s, const float* bounds, int64_t bstride, int n_kv, int n_cand, int k, int cand_offset,
+                      int32_t* out_idx, int64_t idx_stride) {
+  if (n_cand <= kMaxCand) {
+    hipLaunchKernelGGL(select_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k, cand_offset, 0, out_idx,
+                       idx_stride);
+  } else {
+    hipLaunchKernelGGL(select_stream_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k, cand_offset, 0,
+                       out_idx, idx_stride);
+  }
+  LKV_CHECK_LAUNCH("select");
+  return LKV_OK;
+}
+
 extern "C" int lkv_bound_topk(uintptr_t stream, const void* q, int q_dtype, const void* kmin, const void* kmax,
                               int meta_dtype, int64_t meta_head_stride, int n_q, int n_kv, int head_dim,
                               int cand_offset, int n_cand, int k, int rank_mode, int flags, int32_t* out_idx,
@@ -667,18 +697,8 @@ extern "C" int lkv_bound_topk(uintptr_t stream, const void* q, int q_dtype, cons
   }
   const int g = n_q / n_kv;
   hipStream_t s = (hipStream_t)stream;
-  int rc;
-  if (head_dim == 128) {
-    rc = meta_dtype == LKV_BF16 ? dispatch_g<128, LKV_BF16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv,
-                                                             cand_offset, n_cand, rank_mode, bounds, bstride)
-                                : dispatch_g<128, LKV_F16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv,
-                                                            cand_offset, n_cand, rank_mode, bounds, bstride);
-  } else {
-    rc = meta_dtype == LKV_BF16 ? dispatch_g<64, LKV_BF16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv,
-                                                            cand_offset, n_cand, rank_mode, bounds, bstride)
-                                : dispatch_g<64, LKV_F16>(g, s, q, q_dtype, kmin, kmax, meta_head_stride, n_kv,
-                                                           cand_offset, n_cand, rank_mode, bounds, bstride);
-  }
+  const int rc = lkv_launch_bounds(s, q, q_dtype, kmin, kmax, meta_dtype, meta_head_stride, n_kv, g, head_dim, cand_offset, n_cand,
+                                   rank_mode, bounds, bstride);
   if (rc != LKV_OK || k == 0) return rc;
   if (n_cand <= kMaxCand) {
     hipLaunchKernelGGL(select_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k, cand_offset,

@@ -246,6 +246,77 @@ def sparse_decode(
     return out, lse
 
 
+# -- a1 + a2 + a5 + a6: bound, top-K and decode of one layer in one call ----------------------------
+
+
+def _select_desc(q: torch.Tensor, n_kv: int, block_size: int, scale: float, k: int, sink_block: int, cur_block: int, fill: int) -> _lib.DecodeDesc:
+    n_q, d = q.reshape(-1, q.shape[-1]).shape
+    return _lib.DecodeDesc(n_q, n_kv, d, block_size, float(scale), k, 1, sink_block, cur_block, fill, 0, 0)
+
+
+class PreparedSelectDecode:
+    """`lkv_select_decode` with its arguments converted once: the Quest bound of candidates
+    cand_offset .. cand_offset + n_cand - 1 from metadata `[1, h, cap, d]`, the top k per head, and
+    the block-sparse decode over sink + selected (from `sel`) + current. `desc.fill` /
+    `desc.cur_block` and `n_cand` (`set_candidates`, within `max_cand`) may change between calls."""
+
+    def __init__(self, q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, block_size: int,
+                 scale: float, sel: Source, sink: Source | None, sink_block: int, cur: Source | None, cur_block: int, fill: int,
+                 out: torch.Tensor, lse: torch.Tensor, rank_mode: int = _lib.RANK_F32, out_idx: torch.Tensor | None = None,
+                 ws: Workspace | None = None, max_cand: int | None = None) -> None:
+        _lib.require_cuda(q, kmin, kmax, out, lse)
+        n_kv, cap, d, hs = _meta_layout(kmin, kmax)
+        qq = q.reshape(-1, d)
+        if not qq.is_contiguous() or qq.shape[0] % n_kv:
+            raise ValueError("query must be contiguous [n_q, d] with n_q a multiple of the KV heads")
+        if cand_offset < 0 or n_cand <= 0 or cand_offset + n_cand > cap or not 0 < k <= n_cand:
+            raise ValueError(f"candidates {cand_offset}..{cand_offset + n_cand} of {cap} metadata blocks, k={k}")
+        if not out.is_contiguous() or out.numel() != qq.numel() or not lse.is_contiguous() or lse.numel() != qq.shape[0] or lse.dtype != torch.float32:
+            raise ValueError("out must be contiguous [n_q, d] and lse contiguous float32 [n_q]")
+        if out_idx is not None and (out_idx.dtype != torch.int32 or tuple(out_idx.shape) != (n_kv, k) or not out_idx.is_contiguous()):
+            raise ValueError(f"out_idx must be contiguous int32 [{n_kv}, {k}]")
+        self.desc = _select_desc(qq, n_kv, block_size, scale, k, sink_block, cur_block, fill)
+        ws = ws or default_workspace(q.device)
+        sizing = max(n_cand, max_cand or 0)
+        ws_ptr, ws_n = ws.get(_lib.lib().lkv_select_decode_workspace_bytes(ctypes.byref(self.desc), sizing))
+        self._c = [s.c() if s is not None else None for s in (sel, sink, cur)]
+        refs = [ctypes.byref(c) if c is not None else None for c in self._c]
+        self._keep = (q, kmin, kmax, out, lse, out_idx, ws.buf, sel, sink, cur)
+        self._fn = _lib.lib().lkv_select_decode
+        self._head = (ctypes.byref(self.desc), qq.data_ptr(), _lib.dtype_code(qq.dtype), address(kmin[0] if kmin.ndim == 4 else kmin),
+                      address(kmax[0] if kmax.ndim == 4 else kmax), _lib.dtype_code(kmin.dtype), hs, cand_offset)
+        self._tail = (rank_mode, refs[0], refs[1], refs[2], out.data_ptr(), _lib.dtype_code(out.dtype), lse.data_ptr(),
+                      out_idx.data_ptr() if out_idx is not None else None, k, ws_ptr, ws_n)
+        self.n_cand = n_cand
+        self._cap = cap - cand_offset
+        self.device = q.device
+
+    def set_candidates(self, n_cand: int) -> None:
+        if not self.desc.k <= n_cand <= self._cap:
+            raise ValueError(f"{n_cand} candidates for k={self.desc.k}")
+        self.n_cand = n_cand
+
+    def __call__(self) -> None:
+        rc = self._fn(torch.cuda.current_stream(self.device).cuda_stream, *self._head, self.n_cand, *self._tail)
+        if rc:
+            _lib.check(rc, "select_decode")
+
+
+def select_decode(q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, block_size: int, scale: float,
+                  sel: Source, sink: Source | None = None, sink_block: int = -1, cur: Source | None = None, cur_block: int = -1, fill: int = 0,
+                  rank_mode: int = _lib.RANK_F32, out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None, lse: torch.Tensor | None = None,
+                  out_idx: torch.Tensor | None = None, ws: Workspace | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Bound + top-k + block-sparse decode of one layer (lkv_select_decode). Returns (out [n_q, d], lse [n_q])."""
+    qq = q.reshape(-1, q.shape[-1]).contiguous()
+    n_q, d = qq.shape
+    out_dtype = out_dtype or (out.dtype if out is not None else qq.dtype)
+    out = out if out is not None else torch.empty((n_q, d), dtype=out_dtype, device=q.device)
+    lse = lse if lse is not None else torch.empty((n_q,), dtype=torch.float32, device=q.device)
+    PreparedSelectDecode(qq, kmin, kmax, k, cand_offset=cand_offset, n_cand=n_cand, block_size=block_size, scale=scale, sel=sel, sink=sink,
+                         sink_block=sink_block, cur=cur, cur_block=cur_block, fill=fill, out=out, lse=lse, rank_mode=rank_mode, out_idx=out_idx, ws=ws)()
+    return out, lse
+
+
 # -- hybrid residency: hits from HBM slots, misses read in place and admitted -------------------------
 
 
@@ -428,22 +499,27 @@ class PreparedBoundTopk:
     capture into a HIP graph: the stream is read at call time.
     """
 
-    def __init__(self, q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, out_idx: torch.Tensor, rank_mode: int = _lib.RANK_F32, ws: Workspace | None = None) -> None:
-        _lib.require_cuda(q, kmin, kmax, out_idx)
+    def __init__(self, q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, out_idx: torch.Tensor | None = None,
+                 rank_mode: int = _lib.RANK_F32, ws: Workspace | None = None, out_bound: torch.Tensor | None = None) -> None:
+        """k == 0 with `out_bound` [h, n_cand] float32: the bounds only."""
+        _lib.require_cuda(q, kmin, kmax)
         n_kv, cap, d, hs = _meta_layout(kmin, kmax)
         if cand_offset < 1 or cand_offset + n_cand > cap or k > n_cand:
             raise ValueError("candidate range outside the metadata, or k > n_cand")
-        if out_idx.dtype != torch.int32 or tuple(out_idx.shape) != (n_kv, k) or not out_idx.is_contiguous():
+        if k > 0 and (out_idx is None or out_idx.dtype != torch.int32 or tuple(out_idx.shape) != (n_kv, k) or not out_idx.is_contiguous()):
             raise ValueError(f"out_idx must be contiguous int32 [{n_kv}, {k}]")
+        if k == 0 and (out_bound is None or out_bound.dtype != torch.float32 or tuple(out_bound.shape) != (n_kv, n_cand) or not out_bound.is_contiguous()):
+            raise ValueError(f"bounds only: out_bound must be contiguous float32 [{n_kv}, {n_cand}]")
         qq = q.reshape(-1, d)
         if not qq.is_contiguous() or qq.shape[0] % n_kv:
             raise ValueError("query must be contiguous [n_q, d] with n_q a multiple of the KV heads")
         ws = ws or default_workspace(q.device)
         ws_ptr, ws_n = ws.get(_lib.lib().lkv_bound_topk_workspace_bytes(n_kv, n_cand, k))
-        self._keep = (q, kmin, kmax, out_idx, ws.buf)
+        self._keep = (q, kmin, kmax, out_idx, out_bound, ws.buf)
         self._fn = _lib.lib().lkv_bound_topk
         self._args = (qq.data_ptr(), _lib.dtype_code(qq.dtype), address(kmin[0] if kmin.ndim == 4 else kmin), address(kmax[0] if kmax.ndim == 4 else kmax),
-                      _lib.dtype_code(kmin.dtype), hs, qq.shape[0], n_kv, d, cand_offset, n_cand, k, rank_mode, 0, out_idx.data_ptr(), k, None, ws_ptr, ws_n)
+                      _lib.dtype_code(kmin.dtype), hs, qq.shape[0], n_kv, d, cand_offset, n_cand, k, rank_mode, 0,
+                      out_idx.data_ptr() if out_idx is not None else None, max(k, 1), out_bound.data_ptr() if out_bound is not None else None, ws_ptr, ws_n)
         self.device = q.device
 
     def __call__(self) -> None:

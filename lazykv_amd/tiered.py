@@ -460,17 +460,36 @@ class TieredLayer:
         idx = kernels.bound_topk(query, self.kmin, self.kmax, self.k, cand_offset=1, n_cand=n_full - 1, rank_mode=self.rank_mode, sorted_=True)
         return idx.to(torch.int64).cpu().numpy()
 
+    def fused_select(self) -> bool:
+        """Whether a decode without given ids makes the whole step one call (lkv_select_decode):
+        zero-copy or resident reads, no exact remainder."""
+        n_full, _ = self.candidates()
+        return self.res is None and not self.exact and self.k <= n_full - 1
+
     def decode(self, query: torch.Tensor, scaling: float | None, idx: torch.Tensor | None = None, out: torch.Tensor | None = None, lse: torch.Tensor | None = None, ws: kernels.Workspace | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-        """Attention of one decode token over this layer's attended set. Returns out [n_q, d], lse [n_q]."""
+        """Attention of one decode token over this layer's attended set. Returns out [n_q, d], lse [n_q].
+
+        Without `idx`, the selection is made here: in the same call as the attention where
+        `fused_select` allows (lkv_select_decode), else by `rank` first."""
+        n_full, fill = self.candidates()
+        scale = scaling if scaling is not None else self.d**-0.5
+        if idx is None and self.fused_select():
+            qq = query.reshape(-1, self.d)
+            if not qq.is_contiguous():
+                qq = qq.contiguous()
+            out = out if out is not None else torch.empty(qq.shape, dtype=qq.dtype, device=qq.device)
+            lse = lse if lse is not None else torch.empty((qq.shape[0],), dtype=torch.float32, device=qq.device)
+            sel = self._store_src if self.fetch == "resident" else self._host_src
+            return kernels.select_decode(qq, self.kmin, self.kmax, self.k, cand_offset=1, n_cand=n_full - 1, block_size=self.bs, scale=scale, sel=sel,
+                                         sink=self._pool_src, sink_block=0, cur=self._pool_src, cur_block=1 if fill > 0 else -1, fill=fill,
+                                         rank_mode=self.rank_mode, out=out, lse=lse, ws=ws)
         if idx is None:
             idx = self.rank(query, ws=ws)
-        n_full, fill = self.candidates()
         sel = self._store_src if self.fetch == "resident" else self._host_src
         rem = None
         rem_range = (0, 0)
         if self.exact:
             rem, rem_range = self._host_src, (1, n_full)
-        scale = scaling if scaling is not None else self.d**-0.5
         if self.res is not None:
             return kernels.hybrid_decode(
                 query.reshape(-1, self.d), n_kv=self.h, block_size=self.bs, scale=scale, host=self._host_src, res=self.res, idx=idx,
@@ -610,8 +629,11 @@ class TieredCache(Cache):
         tier = self.tiers.get(layer_idx)
         if tier is None or query.shape[-2] != 1:
             return None
-        idx = tier.rank(query, out=self._idx, ws=self._ws)
-        out, lse = tier.decode(query, scaling, idx=idx, ws=self._ws)
+        if tier.fused_select():
+            out, lse = tier.decode(query, scaling, ws=self._ws)
+        else:
+            idx = tier.rank(query, out=self._idx, ws=self._ws)
+            out, lse = tier.decode(query, scaling, idx=idx, ws=self._ws)
         c = self.counters
         c.selections += 1
         c.selected_pairs += tier.h * tier.k

@@ -78,6 +78,14 @@ def test_bad_arguments_are_rejected_before_any_launch(lib) -> None:  # noqa: ANN
     desc = _lib.DecodeDesc(32, 8, 128, 260, 0.088, 0, 1, 0, -1, 1, 0, 0)  # past the largest block size (256)
     rc = lib.lkv_sparse_decode(0, ctypes.byref(desc), dummy, _lib.BF16, None, None, 0, None, None, None, dummy, _lib.BF16, dummy, dummy, 1 << 20)
     assert rc == _lib.LKV_ERR_INVALID and b"block_size" in lib.lkv_last_error()
+    # The one-call decode step: more candidates than any selection takes, k past them.
+    desc = _lib.DecodeDesc(32, 8, 128, 16, 0.088, 512, 1, 0, 1, 16, 0, 0)
+    rc = lib.lkv_select_decode(0, ctypes.byref(desc), dummy, _lib.BF16, dummy, dummy, _lib.BF16, 1 << 30, 1, 300000, 0, None, None, None,
+                               dummy, _lib.BF16, dummy, None, 0, dummy, 1 << 30)
+    assert rc == _lib.LKV_ERR_INVALID and b"300000 candidate blocks" in lib.lkv_last_error()
+    rc = lib.lkv_select_decode(0, ctypes.byref(desc), dummy, _lib.BF16, dummy, dummy, _lib.BF16, 1 << 24, 1, 500, 0, None, None, None,
+                               dummy, _lib.BF16, dummy, None, 0, dummy, 1 << 24)
+    assert rc == _lib.LKV_ERR_INVALID and b"k=512" in lib.lkv_last_error()
 
 
 def test_errors_map_to_the_reference_exception_types() -> None:

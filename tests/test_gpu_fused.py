@@ -1,0 +1,190 @@
+"""The one-call decode step (lkv_select_decode: the bound kernel, then the top K chosen inside the
+decode launch up to 4,096 candidates per head, or by its own launch beyond) against the
+two-entry-point path (lkv_bound_topk, then lkv_sparse_decode) and against the oracle: the selected
+ids are identical, the outputs equal bit for bit (the same plan and partials), and both match the
+float64 oracle within the 2e-3 bar (lazykv/selection.py:38-62, lazykv/attention.py:97-136)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _f64(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _layer(seed: int, h: int, g: int, n: int, bs: int, d: int, dt: torch.dtype):
+    """A layer as the tier holds it: pool [n, h, 2, bs, d] (block n - 1 is the current one) and the
+    metadata of blocks 0..n-1 [1, h, n, d]."""
+    from lazykv_amd.workload import draw_layer, to_pool
+
+    w = draw_layer(seed, h * g, h, d, n * bs, bs, dt)
+    pool = to_pool(w.keys, w.values, bs)
+    blocks = w.keys.view(h, n, bs, d)  # exact per-channel extremes, representable in the model dtype
+    kmin = blocks.amin(dim=2)[None].cuda()
+    kmax = blocks.amax(dim=2)[None].cuda()
+    return w, pool, kmin, kmax
+
+
+CASES = [
+    # (KV heads, group, blocks, block size, head dim, k, fill, dtype, where the selected pairs live)
+    (8, 4, 8192, 16, 128, 512, 16, torch.bfloat16, "host"),  # the 128K-token 8B-shaped layer, zero-copy
+    (8, 4, 8192, 16, 128, 512, 16, torch.bfloat16, "hbm"),
+    (8, 4, 2048, 16, 64, 512, 16, torch.float16, "hbm"),  # the 32K-token 1B-shaped layer
+    (8, 4, 4096, 16, 64, 1024, 16, torch.float16, "int8-hbm"),  # the 64K-token int8 tier
+    (8, 4, 300, 16, 128, 64, 5, torch.bfloat16, "int8-host"),
+    (2, 8, 500, 16, 128, 37, 9, torch.bfloat16, "hbm"),
+    (4, 2, 130, 32, 64, 100, 1, torch.float16, "host"),
+    (1, 4, 700, 16, 64, 3, 16, torch.bfloat16, "hbm"),
+    (4, 1, 60, 64, 128, 58, 60, torch.float16, "hbm"),  # every candidate selected
+    (2, 4, 4098, 16, 64, 300, 3, torch.bfloat16, "hbm"),  # 4,096 candidates: the most selected inside the decode launch
+    (2, 4, 4099, 16, 64, 300, 3, torch.bfloat16, "hbm"),  # 4,097: the top-K in its own launch
+    (1, 8, 20002, 16, 64, 700, 12, torch.float16, "host"),  # 20,000: the streaming top-K
+]
+
+
+@pytest.mark.parametrize(("h", "g", "n", "bs", "d", "k", "fill", "dt", "where"), CASES)
+def test_select_decode_equals_the_two_launch_path_and_the_oracle(h: int, g: int, n: int, bs: int, d: int, k: int, fill: int, dt: torch.dtype, where: str) -> None:
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+    from lazykv_amd.quant import packed_pair_bytes
+
+    print(f"fused decode case: h={h} g={g} n={n} bs={bs} d={d} k={k} fill={fill} {dt} {where}", flush=True)
+    w, pool, kmin, kmax = _layer(n * 7 + d + k, h, g, n, bs, d, dt)
+    n_cand = n - 2  # blocks 1 .. n - 2; block n - 1 is the current block
+    tag = "bf16" if dt == torch.bfloat16 else "f16"
+    if where.startswith("int8"):
+        recs = R.pack(_bits(pool), tag)
+        store = pinned_empty((n, h, packed_pair_bytes(bs, d)), torch.uint8) if where.endswith("host") else torch.empty((n, h, packed_pair_bytes(bs, d)), dtype=torch.uint8, device="cuda")
+        store.copy_(torch.from_numpy(recs))
+        sel = kernels.record_source(store, dt)
+        deq_bits = R.unpack(recs.reshape(n * h, -1), bs, d, tag).reshape(n, h, 2, bs, d)
+
+        def stored(b, j):
+            x = R.to_f32(deq_bits[b, j], tag).astype(np.float64)
+            return x[0], x[1]
+    else:
+        store = pinned_empty(tuple(pool.shape), dt) if where == "host" else pool.cuda()
+        if where == "host":
+            store.copy_(pool)
+        sel = kernels.pool_source(store)
+
+        def stored(b, j):
+            x = _f64(pool[b, j])
+            return x[0], x[1]
+    slots = pool[[0, n - 1]].contiguous().cuda()
+    ss = kernels.pool_source(slots)
+    q = w.query.cuda()
+    scale = d**-0.5
+    common = dict(block_size=bs, scale=scale, sel=sel, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=fill)
+    idx_f = torch.full((h, k), -1, dtype=torch.int32, device="cuda")
+    ws = kernels.Workspace()
+    out_f, lse_f = kernels.select_decode(q, kmin, kmax, k, cand_offset=1, n_cand=n_cand, out_idx=idx_f, out_dtype=torch.float32, ws=ws, **common)
+    idx_2 = kernels.bound_topk(q, kmin, kmax, k, cand_offset=1, n_cand=n_cand, ws=ws)
+    out_2, lse_2 = kernels.sparse_decode(q, n_kv=h, idx=idx_2, out_dtype=torch.float32, ws=ws, **common)
+    # Once more on the same workspace, after the two-call path used it.
+    out_g, lse_g = kernels.select_decode(q, kmin, kmax, k, cand_offset=1, n_cand=n_cand, out_dtype=torch.float32, ws=ws, **common)
+    torch.cuda.synchronize()
+    assert torch.equal(idx_f, idx_2)
+    assert torch.equal(out_f, out_2) and torch.equal(lse_f, lse_2)
+    assert torch.equal(out_g, out_f) and torch.equal(lse_g, lse_f)
+    # The oracle: the selected set (near-tie rule) and the attention over it.
+    bound = R.quest_bound(_f64(w.query), _f64(kmin[0, :, 1 : n - 1]), _f64(kmax[0, :, 1 : n - 1]))
+    chosen = idx_f.cpu().numpy()
+    for j in range(h):
+        assert (np.diff(chosen[j]) > 0).all(), j  # ascending, distinct
+        ok, _ = R.selection_ok(chosen[j] - 1, bound[j], k, abs_err=1e-3)
+        assert ok, j
+
+    def bkv(j, b):
+        if b in (0, n - 1):  # sink and current block stay in the model dtype
+            x = _f64(pool[b, j])
+            return x[0], x[1]
+        return stored(b, j)
+
+    ks, vs = R.gathered_tokens(bkv, h, chosen, 0, n - 1, fill, bs)
+    want_o, want_l = R.attend_tokens(_f64(w.query), ks, vs, scale)
+    assert np.abs(out_f.cpu().numpy() - want_o).max() < TOL
+    assert np.abs(lse_f.cpu().numpy() - want_l).max() < TOL
+
+
+def test_fused_step_replays_in_a_graph_like_the_eager_call() -> None:
+    """The one-call step captured in a HIP graph (bound kernel, the decode launch choosing the top K,
+    the merge launch): every replay, with unrelated eager work and synchronisations between replays,
+    equals the eager result bit for bit."""
+    from lazykv_amd import kernels
+
+    h, g, n, bs, d, k = 8, 4, 1030, 16, 128, 128
+    w, pool, kmin, kmax = _layer(99, h, g, n, bs, d, torch.bfloat16)
+    store = pool.cuda()
+    src = kernels.pool_source(store)
+    ss = kernels.pool_source(pool[[0, n - 1]].contiguous().cuda())
+    q = w.query.cuda()
+    out = torch.empty((h * g, d), dtype=torch.float32, device="cuda")
+    lse = torch.empty((h * g,), dtype=torch.float32, device="cuda")
+    step = kernels.PreparedSelectDecode(q, kmin, kmax, k, cand_offset=1, n_cand=n - 2, block_size=bs, scale=d**-0.5, sel=src, sink=ss, sink_block=0,
+                                        cur=ss, cur_block=1, fill=7, out=out, lse=lse, ws=kernels.Workspace())
+    step()
+    torch.cuda.synchronize()
+    want_o, want_l = out.clone(), lse.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(5):
+        out.zero_()
+        lse.zero_()
+        noise = torch.randn(1 << 20, device="cuda").sum()  # unrelated eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        assert torch.equal(out, want_o) and torch.equal(lse, want_l), rep
+
+
+def test_tier_takes_the_fused_launch_and_agrees_with_rank_then_decode() -> None:
+    """TieredCache.select decodes through lkv_select_decode (one call per selecting layer); its
+    output equals rank() + decode(idx) (the two-entry-point path) bit for bit."""
+    from lazykv_amd.tiered import TieredCache
+
+    h, g, d, bs, k = 8, 4, 128, 16, 24
+    gen = torch.Generator().manual_seed(5)
+    keys = (torch.randn((1, h, 700, d), generator=gen) * 1.3).to(torch.bfloat16).cuda()
+    values = torch.randn((1, h, 700, d), generator=gen).to(torch.bfloat16).cuda()
+    for fetch in ("zerocopy", "resident"):
+        cache = TieredCache([(keys, values)] * 2, k, bs, 1024, dense_layers=1, fetch=fetch)
+        tier = cache.tiers[1]
+        assert tier.fused_select()
+        q = torch.randn((1, h * g, 1, d), generator=gen).to(torch.bfloat16).cuda()
+        dec = cache.select(1, q)
+        idx = tier.rank(q)
+        out2, lse2 = tier.decode(q, None, idx=idx)
+        torch.cuda.synchronize()
+        assert torch.equal(dec.out.view(h * g, d), out2) and torch.equal(dec.lse.view(-1), lse2), fetch
+
+
+def test_select_decode_refuses_what_it_cannot_do() -> None:
+    from lazykv_amd import kernels
+
+    h, d, bs = 2, 64, 16
+    kmin = torch.zeros((1, h, 300, d), dtype=torch.float16, device="cuda")
+    pool = torch.zeros((4, h, 2, bs, d), dtype=torch.float16, device="cuda")
+    src = kernels.pool_source(pool)
+    q = torch.zeros((h * 4, d), dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):  # nothing selected
+        kernels.select_decode(q, kmin, kmin, 0, cand_offset=1, n_cand=100, block_size=bs, scale=0.1, sel=src)
+    with pytest.raises(ValueError):  # more selected than there are candidates
+        kernels.select_decode(q, kmin, kmin, 101, cand_offset=1, n_cand=100, block_size=bs, scale=0.1, sel=src)
+    with pytest.raises(ValueError):  # candidates past the metadata
+        kernels.select_decode(q, kmin, kmin, 10, cand_offset=1, n_cand=300, block_size=bs, scale=0.1, sel=src)
