@@ -125,18 +125,28 @@ struct RawI8 {
   uint32_t vz[NI];
 };
 
+// Every pair this file reads -- HBM or mapped host memory -- is global memory. Reads through this
+// cast compile to global loads even where the pointer was picked at run time; a generic pointer
+// compiles to flat loads, whose waits also wait on the LDS counter.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const void* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+
 template <int W>
 __device__ __forceinline__ void load_words(const void* p, uint32_t (&w)[W]) {
   if constexpr (W == 1) {
-    w[0] = *(const uint32_t*)p;
+    w[0] = *gmem<uint32_t>(p);
   } else if constexpr (W == 2) {
-    const uint2 x = *(const uint2*)p;
+    const u32x2 x = *gmem<u32x2>(p);
     w[0] = x.x;
     w[1] = x.y;
   } else {
 #pragma unroll
     for (int i = 0; i < W / 4; ++i) {
-      const uint4 x = ((const uint4*)p)[i];
+      const u32x4 x = gmem<u32x4>(p)[i];
       w[4 * i] = x.x;
       w[4 * i + 1] = x.y;
       w[4 * i + 2] = x.z;
@@ -157,18 +167,16 @@ __device__ __forceinline__ void load_raw(const Src& s, int block, int h, int t0,
 #pragma unroll
   for (int i = 0; i < L::NI; ++i) {
     // Branch-free: a row past `limit` (which may lie past the end of the source) reads the
-    // block's row 0 instead and is zeroed. Loads under a branch, zeros on the other, were merged
-    // by the compiler into stores through a computed address, which kept `raw` in private memory.
+    // block's row 0 instead. Its registers keep what was read: every consumer masks such rows by
+    // selection (scores excluded, values skipped), so nothing waits on the load here and the
+    // loads of the next pair issue behind these without a pause. (Loads under a branch were
+    // merged by the compiler into stores through a computed address, which kept `raw` in
+    // private memory.)
     const int row = t0 + r + L::RG * i;
     const bool ok = i < nit && row < limit;
     const int64_t at = (int64_t)(ok ? row : 0) * D;
     load_words(kb + at, raw.k[i]);
     load_words(vb + at, raw.v[i]);
-#pragma unroll
-    for (int w = 0; w < RawModel<D, MT>::W; ++w) {
-      raw.k[i][w] = ok ? raw.k[i][w] : 0u;
-      raw.v[i][w] = ok ? raw.v[i][w] : 0u;
-    }
   }
 }
 
@@ -236,16 +244,12 @@ __device__ __forceinline__ void load_raw(const Src& s, int bs, int block, int h,
     // Rows past `limit` are masked before their values are used.
     raw.vs[i] = (row & 1) ? wvs[i] >> 16 : wvs[i] & 0xffffu;
     raw.vz[i] = (row & 1) ? wvz[i] >> 16 : wvz[i] & 0xffffu;
-    // Branch-free as for model-dtype rows: a masked row reads row 0 of the record and is zeroed.
+    // Branch-free as for model-dtype rows: a masked row reads row 0 of the record, and its
+    // consumers mask it.
     const bool ok = i < nit && row < limit;
     const int at = (ok ? row : 0) * D + c * EPL;
     load_words(rec + at, raw.k[i]);
     load_words(rec + bs * D + at, raw.v[i]);
-#pragma unroll
-    for (int w = 0; w < RawI8<D>::W; ++w) {
-      raw.k[i][w] = ok ? raw.k[i][w] : 0u;
-      raw.v[i][w] = ok ? raw.v[i][w] : 0u;
-    }
   }
 }
 
@@ -492,14 +496,12 @@ __device__ __forceinline__ void load_raw_mf(const Src& s, int block, int h, int 
   const int kr = t0 + lane % 16;
   const uint16_t* krow = kb + (int64_t)(kr < limit ? kr : 0) * D + 8 * (lane / 16);
 #pragma unroll
-  for (int st = 0; st < D / 32; ++st) raw.k[st] = __builtin_bit_cast(typename Mfma<MT>::V8, *(const uint4*)(krow + 32 * st));
+  for (int st = 0; st < D / 32; ++st) raw.k[st] = __builtin_bit_cast(typename Mfma<MT>::V8, *gmem<u32x4>(krow + 32 * st));
 #pragma unroll
   for (int i = 0; i < L::NI; ++i) {
     const int row = t0 + r + L::RG * i;
     const bool ok = i < nit && row < limit;
-    load_words(vb + (int64_t)(ok ? row : 0) * D + c * EPL, raw.v[i]);
-#pragma unroll
-    for (int w = 0; w < RawModel<D, MT>::W; ++w) raw.v[i][w] = ok ? raw.v[i][w] : 0u;
+    load_words(vb + (int64_t)(ok ? row : 0) * D + c * EPL, raw.v[i]);  // masked in consume_mf
   }
 }
 
@@ -638,13 +640,37 @@ __device__ __forceinline__ void process_items_mf(const DecodeArgs& a, const Src 
   int lk[NP];  // valid tokens per pair; 0 for a skipped pair
 #pragma unroll
   for (int u = 0; u < NP; ++u) lk[u] = ok[u] ? lim[u] : 0;
+  // A skipped pair loads the first live pair again (its lk of 0 masks it), so every pair's loads
+  // are issued unconditionally, back to back: under a per-pair branch the compiler put waits
+  // between one pair's loads and the next (registers of in-flight loads reused across the
+  // branches), and the pairs of a round arrived one memory latency apart.
+  // The first live pair, picked by unrolled selects (an index into s would put it in scratch).
+  Src fs = s[0];
+  int fb = -1, fl = 0;
+#pragma unroll
+  for (int u = NP - 1; u >= 0; --u) {
+    if (ok[u]) {
+      fs = s[u];
+      fb = blk[u];
+      fl = lim[u];
+    }
+  }
+  if (fb < 0) return;  // wave-uniform: nothing live
+  Src ls[NP];
+  int lb[NP], ll[NP];
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    ls[u] = ok[u] ? s[u] : fs;
+    lb[u] = ok[u] ? blk[u] : fb;
+    ll[u] = ok[u] ? lim[u] : fl;
+  }
 #pragma unroll 1
   for (int t0 = 0; t0 < a.bs; t0 += 16) {
     const int nit = min(Lanes<D>::NI, (a.bs - t0 + Lanes<D>::RG - 1) / Lanes<D>::RG);
     RawMf<D, MT> raw[NP];
 #pragma unroll
-    for (int u = 0; u < NP; ++u)
-      if (ok[u]) load_raw_mf<D, MT>(s[u], blk[u], h, t0, nit, lim[u], lane, r, c, raw[u]);
+    for (int u = 0; u < NP; ++u) load_raw_mf<D, MT>(ls[u], lb[u], h, t0, nit, ll[u], lane, r, c, raw[u]);
+    __builtin_amdgcn_sched_barrier(0);  // every load above issues before the first use below
     consume_mf<D, MT, G, NP>(qb, raw, a.qscale, t0, nit, lk, lane, r, sp, st);
   }
 }
