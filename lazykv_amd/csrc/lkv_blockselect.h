@@ -5,9 +5,15 @@
 // taken towards the lower candidate index, reported in ascending index order. Each thread holds a
 // contiguous run of up to KPT candidates as order-preserving integer keys. The k-th largest key is
 // found by range-adaptive radix select: a pass histograms the live key range into at most 2048
-// bins scaled to that range and keeps the bin holding the k-th key; once that bin holds at most NT
-// keys they are ranked directly (one thread each) instead of another pass. Three passes narrow
-// any 32-bit range to one value, so the loop is capped at four.
+// bins scaled to that range and keeps the bin holding the k-th key. When that bin's keys are all
+// taken the selection is complete; when it holds at most NT keys they are ranked directly (one
+// thread each) instead of another pass. Three passes narrow any 32-bit range to one value, so the
+// loop is capped at four.
+//
+// Each phase is one LDS round trip and one barrier: a thread owns kSelBins / NT consecutive bins
+// and reads them in one vector load, and the boundary bin is found in registers. (On MI355X an LDS
+// atomic to a random bin costs about one lane per clock when lanes collide on banks, so a key
+// takes part in a pass only while it lies in the live range.)
 #pragma once
 
 #include "lkv_common.h"
@@ -25,8 +31,10 @@ __device__ __forceinline__ uint32_t orderable_key(float f) {
 template <int NT, int KPT>
 struct SelectLds {
   static constexpr int kWaves = NT / 64;
-  static constexpr int kCap = NT * KPT;  // candidates one workgroup can hold
-  uint32_t hist[kSelBins + 64];          // + one spare bin per lane for keys outside the range
+  static constexpr int kCap = NT * KPT;          // candidates one workgroup can hold
+  static constexpr int kBpt = kSelBins / NT;     // bins a thread owns
+  static_assert(kBpt == 2 || kBpt == 4 || kBpt == 8, "256, 512 or 1024 threads");
+  alignas(16) uint32_t hist[kSelBins];
   uint32_t list_key[NT];
   uint32_t list_id[NT];
   uint32_t taken[kCap / 32];  // boundary-bin keys ranked among the best, one bit per candidate
@@ -62,12 +70,41 @@ __device__ __forceinline__ uint32_t workgroup_exclusive_sum(uint32_t v, uint32_t
   return before + x - v;
 }
 
+// A thread's kBpt bins, as vector LDS accesses.
+template <int B>
+__device__ __forceinline__ void read_bins(const uint32_t* p, uint32_t (&c)[B]) {
+#pragma unroll
+  for (int i = 0; i < B; i += 4) {
+    if constexpr (B == 2) {
+      const uint2 x = *(const uint2*)p;
+      c[0] = x.x;
+      c[1] = x.y;
+    } else {
+      const uint4 x = *(const uint4*)(p + i);
+      c[i] = x.x;
+      c[i + 1] = x.y;
+      c[i + 2] = x.z;
+      c[i + 3] = x.w;
+    }
+  }
+}
+template <int B>
+__device__ __forceinline__ void clear_bins(uint32_t* p) {
+  if constexpr (B == 2) {
+    *(uint2*)p = make_uint2(0u, 0u);
+  } else {
+#pragma unroll
+    for (int i = 0; i < B; i += 4) *(uint4*)(p + i) = make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
 // Select k of the n bounds at `bound_h` (n <= NT * KPT; the row is readable in whole 16-byte
 // vectors up to a multiple of 4 when `aligned`). Every thread of the workgroup must call it.
 template <int NT, int KPT>
 __device__ __forceinline__ SelectPick block_top_k(const float* __restrict__ bound_h, bool aligned, int n, int k, SelectLds<NT, KPT>& L) {
   static_assert(KPT % 4 == 0 && KPT <= 32, "a thread's slots are tracked in 32-bit masks, loaded 4 at a time");
   constexpr int kWaves = NT / 64;
+  constexpr int kBpt = SelectLds<NT, KPT>::kBpt;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // Keys per thread: a multiple of 4, so a thread's run is whole 16-byte vectors.
   const int npt = ((n + NT - 1) / NT + 3) & ~3;
@@ -88,14 +125,17 @@ __device__ __forceinline__ SelectPick block_top_k(const float* __restrict__ boun
 #pragma unroll
     for (int u = 0; u < KPT; ++u) key[u] = u < nlive ? orderable_key(bound_h[i0 + u]) : 0u;
   }
-  // While the loads are in flight: clear the bitmap and the first pass's histogram.
+  uint32_t live = 0u;  // bit u: slot u holds a candidate
+#pragma unroll
+  for (int u = 0; u < KPT; ++u) live |= (u < nlive ? 1u : 0u) << u;
+  // While the loads are in flight: clear the bitmap and this thread's bins for the first pass.
   for (int i = threadIdx.x; i < SelectLds<NT, KPT>::kCap / 32; i += NT) L.taken[i] = 0u;
-  for (int i = threadIdx.x; i < kSelBins; i += NT) L.hist[i] = 0u;
+  clear_bins<kBpt>(L.hist + threadIdx.x * kBpt);
   uint32_t lmin = 0xffffffffu, lmax = 0u;
 #pragma unroll
   for (int u = 0; u < KPT; ++u) {
-    lmin = min(lmin, u < nlive ? key[u] : 0xffffffffu);
-    lmax = max(lmax, u < nlive ? key[u] : 0u);
+    lmin = min(lmin, ((live >> u) & 1u) ? key[u] : 0xffffffffu);
+    lmax = max(lmax, ((live >> u) & 1u) ? key[u] : 0u);
   }
   lmin = wave_min_u32(lmin);
   lmax = wave_max_u32(lmax);
@@ -111,51 +151,45 @@ __device__ __forceinline__ SelectPick block_top_k(const float* __restrict__ boun
     hi = max(hi, L.mm[2 * w + 1]);
   }
 
-  int need = k;          // keys still to take from [lo, hi]; every key above hi is taken
-  uint32_t T = lo;       // after the loop: keys > T are taken, `need` of the keys == T, and the marked ones
+  // After the loop: every key above hi is taken, and of the keys in [lo, hi] either all
+  // (whole), the marked ones (ranked), or -- when lo == hi, or the pass cap was reached -- the
+  // first `need` keys equal to lo in index order.
+  int need = k;
+  bool whole = false, ranked = false;
   uint32_t marked = 0u;  // bit u: key[u] was ranked among the boundary bin's best
 #pragma unroll 1
   for (int pass = 0; pass < kSelPasses; ++pass) {
-    if (lo >= hi) {
-      T = lo;
-      break;
-    }
+    if (lo >= hi) break;
     const uint32_t width = hi - lo;
     const int bits = 32 - __clz(width);
     const int shift = bits > 11 ? bits - 11 : 0;
-    const int nb = (int)(width >> shift) + 1;
-    if (pass > 0) {
-      for (int i = threadIdx.x; i < nb; i += NT) L.hist[i] = 0u;
+    if (pass > 0) {  // the previous pass read its bins before the barrier that published `info`
+      clear_bins<kBpt>(L.hist + threadIdx.x * kBpt);
       __syncthreads();
     }
 #pragma unroll
-    for (int u = 0; u < KPT; ++u) {
-      const bool in = u < nlive && key[u] >= lo && key[u] <= hi;
-      atomicAdd(&L.hist[in ? (key[u] - lo) >> shift : kSelBins + lane], 1u);
-    }
+    for (int u = 0; u < KPT; ++u)
+      if (((live >> u) & 1u) && key[u] >= lo && key[u] <= hi) atomicAdd(&L.hist[(key[u] - lo) >> shift], 1u);
     __syncthreads();
-    const int per = (nb + NT - 1) / NT;  // thread t owns bins [t * per, (t + 1) * per)
+    uint32_t cnt[kBpt];
+    read_bins<kBpt>(L.hist + threadIdx.x * kBpt, cnt);
     uint32_t local = 0;
-    for (int j = 0; j < per; ++j) {
-      const int bin = threadIdx.x * per + j;
-      if (bin < nb) local += L.hist[bin];
-    }
+#pragma unroll
+    for (int b = 0; b < kBpt; ++b) local += cnt[b];
     uint32_t total;
     const uint32_t below = workgroup_exclusive_sum<NT>(local, L.scan[0], &total);
-    const uint32_t above = total - below - local;
+    const uint32_t above = total - below - local;  // keys of higher bins (owned by later threads)
     if (above < (uint32_t)need && (uint32_t)need <= above + local) {
       uint32_t acc = above;
-      for (int j = per - 1; j >= 0; --j) {
-        const int bin = threadIdx.x * per + j;
-        const uint32_t cnt = bin < nb ? L.hist[bin] : 0u;
-        if ((uint32_t)need <= acc + cnt) {
-          L.info[0] = (uint32_t)bin;
+#pragma unroll
+      for (int b = kBpt - 1; b >= 0; --b) {
+        if (acc < (uint32_t)need && (uint32_t)need <= acc + cnt[b]) {
+          L.info[0] = (uint32_t)(threadIdx.x * kBpt + b);
           L.info[1] = acc;
-          L.info[2] = cnt;
+          L.info[2] = cnt[b];
           L.info[3] = 0u;
-          break;
         }
-        acc += cnt;
+        acc += cnt[b];
       }
     }
     __syncthreads();
@@ -166,12 +200,16 @@ __device__ __forceinline__ SelectPick block_top_k(const float* __restrict__ boun
     const uint32_t span = shift ? ((1u << shift) - 1u) : 0u;
     hi = min(hi, new_lo + span);
     lo = new_lo;
+    if (in_bin == (uint32_t)need) {  // the boundary bin is taken whole
+      whole = true;
+      break;
+    }
     if (lo < hi && in_bin <= (uint32_t)NT) {
       // Few keys in the boundary bin: rank them directly by (key desc, index asc) and mark the
       // `need` best in the bitmap, which each thread reads back for its own run.
 #pragma unroll
       for (int u = 0; u < KPT; ++u) {
-        if (u < nlive && key[u] >= lo && key[u] <= hi) {
+        if (((live >> u) & 1u) && key[u] >= lo && key[u] <= hi) {
           const uint32_t slot = atomicAdd(&L.info[3], 1u);
           L.list_key[slot] = key[u];
           L.list_id[slot] = (uint32_t)(i0 + u);
@@ -194,22 +232,22 @@ __device__ __forceinline__ SelectPick block_top_k(const float* __restrict__ boun
       const uint32_t w1 = ((i0 >> 5) + 1) < SelectLds<NT, KPT>::kCap / 32 ? L.taken[(i0 >> 5) + 1] : 0u;
       const uint64_t both = ((uint64_t)w1 << 32) | w0;
       marked = (uint32_t)(both >> (i0 & 31)) & (npt >= 32 ? 0xffffffffu : ((1u << npt) - 1u));
-      T = hi;
-      need = 0;
+      ranked = true;
       break;
     }
-    __syncthreads();  // info and hist are rewritten by the next pass
   }
 
-  // Per thread, the slots taken outright (above T, or marked) and the ties (== T, unmarked).
+  // Per thread, the slots taken outright and the ties (equal to lo, unmarked, in tie mode).
+  const bool tie_mode = !whole && !ranked;
   uint32_t above_m = 0u, tie_m = 0u;
 #pragma unroll
   for (int u = 0; u < KPT; ++u) {
-    const uint32_t mk = (marked >> u) & 1u;
-    const uint32_t lv = u < nlive ? 1u : 0u;
-    above_m |= (lv & ((key[u] > T ? 1u : 0u) | mk)) << u;
-    tie_m |= (lv & (key[u] == T ? 1u : 0u) & (mk ^ 1u)) << u;
+    const uint32_t lv = (live >> u) & 1u;
+    const uint32_t out = (key[u] > hi ? 1u : 0u) | (whole && key[u] >= lo ? 1u : 0u) | (ranked ? (marked >> u) & 1u : 0u);
+    above_m |= (lv & out) << u;
+    tie_m |= (lv & (tie_mode && key[u] == lo ? 1u : 0u)) << u;
   }
+  if (!tie_mode) need = 0;
   const uint32_t gt = __popc(above_m), eq = __popc(tie_m);
   uint32_t tot;
   const uint32_t packed = workgroup_exclusive_sum<NT>((eq << 16) | gt, L.scan[1], &tot);

@@ -759,6 +759,18 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   __shared__ SelLds s_sel;
   using V8 = typename Mfma<MT == LKV_F32 ? LKV_F16 : MT>::V8;
 
+  // The query first: its loads are in flight during the selection below.
+  V8 qb[D / 32];
+  if constexpr (MF) load_query_mf<D, MT, G>(a.q, h, lane, qb);
+  float* sp = s_pb[MF ? wave : 0];
+
+  float q[G][EPL];
+  lkv::load_query_rows<D, G, EPL>(a.q, a.q_dtype, h, c, q);
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) q[j][e] *= a.qscale;
+
   // ---- fused selection: this head's top k, and the ids of this workgroup's run -----------------
   // The run's selected ids go to LDS (over the histogram, free once the selection is done), as
   // positions [sel_base, sel_base + run) of the ascending selected list.
@@ -781,7 +793,7 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       if ((pk.take >> u) & 1u) {
         const int32_t id = pk.i0 + u + a.cand_offset;
         if (pos >= js && pos < je) ids[pos - js] = id;
-        if (out_h != nullptr) out_h[pos] = id;
+        if (out_h != nullptr && pos < a.k) out_h[pos] = id;
         ++pos;
       }
     }
@@ -789,17 +801,6 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     idx_h = ids;
     sel_base = js;
   }
-
-  V8 qb[D / 32];
-  if constexpr (MF) load_query_mf<D, MT, G>(a.q, h, lane, qb);
-  float* sp = s_pb[MF ? wave : 0];
-
-  float q[G][EPL];
-  lkv::load_query_rows<D, G, EPL>(a.q, a.q_dtype, h, c, q);
-#pragma unroll
-  for (int j = 0; j < G; ++j)
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) q[j][e] *= a.qscale;
 
   WaveState<D, G> st;
   st.mh = -INFINITY;

@@ -188,3 +188,69 @@ def test_select_decode_refuses_what_it_cannot_do() -> None:
         kernels.select_decode(q, kmin, kmin, 101, cand_offset=1, n_cand=100, block_size=bs, scale=0.1, sel=src)
     with pytest.raises(ValueError):  # candidates past the metadata
         kernels.select_decode(q, kmin, kmin, 10, cand_offset=1, n_cand=300, block_size=bs, scale=0.1, sel=src)
+
+
+def _designed_bounds(kind: str, n: int, rng: np.random.Generator) -> np.ndarray:
+    """Bounds that exercise each exit of the in-workgroup selection (as bfloat16 values)."""
+    if kind == "all equal":  # one value: ties only, taken in index order
+        b = np.full(n, 1.5)
+    elif kind == "three values":  # the threshold value repeated hundreds of times
+        b = rng.choice([0.5, 1.0, 2.0], size=n)
+    elif kind == "outlier and a dense cluster":
+        # One huge bound stretches the first pass's range so wide that the cluster of every other
+        # bound falls into one bin holding far more keys than threads: a second pass is needed,
+        # whose boundary bin is then ranked directly among heavy ties.
+        b = 1.0 + rng.integers(0, 8, size=n) / 128.0
+        b[n // 3] = 3.0e38
+    elif kind == "distinct":  # every bound different: the boundary bin is taken whole or ranked
+        b = rng.permutation(n).astype(np.float64) / 8.0 - n / 16.0
+    else:  # "negative and zero": signs and a zero mix in the order-preserving keys
+        b = rng.choice([-2.0, -0.0, 0.0, 0.25], size=n)
+    return b
+
+
+DESIGNED = [
+    ("all equal", 2, 4, 1000, 300),
+    ("three values", 2, 4, 4094, 1024),
+    ("outlier and a dense cluster", 1, 4, 4094, 1500),
+    ("distinct", 2, 4, 2046, 512),
+    ("negative and zero", 2, 4, 3000, 1100),
+    ("three values", 1, 8, 4096, 4096),  # every candidate selected
+]
+
+
+@pytest.mark.parametrize(("kind", "h", "g", "n_cand", "k"), DESIGNED)
+def test_selection_inside_the_decode_launch_on_designed_bounds(kind: str, h: int, g: int, n_cand: int, k: int) -> None:
+    """With a one-hot query every bound is exactly one metadata value, so the selected set is known
+    exactly: the k largest, ties towards the lower id. The one-call path, the two-call path (its
+    own selection kernel) and that set agree id for id, and the outputs bit for bit."""
+    from lazykv_amd import kernels
+
+    print(f"designed bounds: {kind} h={h} g={g} n_cand={n_cand} k={k}", flush=True)
+    rng = np.random.default_rng(n_cand + k)
+    bs, d, n = 16, 64, n_cand + 2
+    dt = torch.bfloat16
+    b = _designed_bounds(kind, n_cand, rng)
+    kmax = torch.zeros((1, h, n, d), dtype=dt)
+    for j in range(h):
+        kmax[0, j, 1 : n - 1, 0] = torch.from_numpy(b).to(dt)
+    exact = kmax[0, :, 1 : n - 1, 0].float().numpy().astype(np.float64)  # the bounds the kernels see
+    kmin = kmax.clone()
+    q = torch.zeros((h * g, d), dtype=dt)
+    q[:, 0] = 1.0  # bound = sum_d max(q kmax, q kmin) = kmax[..., 0]
+    pool = (torch.randn((n, h, 2, bs, d), generator=torch.Generator().manual_seed(k)) * 0.5).to(dt)
+    store, kmin, kmax, q = pool.cuda(), kmin.cuda(), kmax.cuda(), q.cuda()
+    sel = kernels.pool_source(store)
+    common = dict(block_size=bs, scale=d**-0.5, sel=sel, sink=sel, sink_block=0, cur=sel, cur_block=n - 1, fill=bs)
+    ws = kernels.Workspace()
+    idx_f = torch.full((h, k), -1, dtype=torch.int32, device="cuda")
+    out_f, lse_f = kernels.select_decode(q, kmin, kmax, k, cand_offset=1, n_cand=n_cand, out_idx=idx_f, out_dtype=torch.float32, ws=ws, **common)
+    idx_2 = kernels.bound_topk(q, kmin, kmax, k, cand_offset=1, n_cand=n_cand, ws=ws)
+    out_2, lse_2 = kernels.sparse_decode(q, n_kv=h, idx=idx_2, out_dtype=torch.float32, ws=ws, **common)
+    torch.cuda.synchronize()
+    for j in range(h):
+        order = np.lexsort((np.arange(n_cand), -exact[j]))  # bound descending, then id ascending
+        want = np.sort(order[:k]) + 1
+        assert np.array_equal(idx_f[j].cpu().numpy(), want), (kind, j)
+    assert torch.equal(idx_f, idx_2)
+    assert torch.equal(out_f, out_2) and torch.equal(lse_f, lse_2)
