@@ -21,7 +21,7 @@ SORTED = 1
 RANK_F32, RANK_MODEL = 0, 1
 HOST_COHERENT = 1
 SRC_HOST = 1
-SELECT_IN_DECODE_MAX_CAND = 4096  # lkv_select_decode chooses the top K inside the decode launch up to this many candidates
+SELECT_IN_DECODE_MAX_CAND = 8192  # lkv_select_decode chooses the top K inside the decode launch up to this many candidates
 STATIC_SCRATCH_BYTES = 16 * 1024 * 1024  # LKV_STATIC_SCRATCH_BYTES: the allocation-free decode's partials per device
 
 _DTYPE_CODES = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}

@@ -731,15 +731,20 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
   }
 }
 
-// Candidates a fused-selection workgroup holds (KPT keys per thread): 4,096 per KV head, a
-// 65,536-token context at 16-token blocks. Longer contexts select in their own launch.
-constexpr int kSelCap = 4096;
-template <int NT>
-constexpr int kSelKpt = kSelCap / NT;
+// Candidates a fused-selection workgroup holds (KPT keys per thread): SEL * kSelUnit per KV head.
+// SEL 1 holds 4,096 (a 65,536-token context at 16-token blocks), SEL 2 holds 8,192; a launch
+// takes the smaller that fits, since every key slot a thread holds costs its instructions in each
+// selection phase (measured: the 32K-token 1B step 1.7 us slower per layer with 8,192 slots than
+// with 4,096). Longer contexts select in their own launch.
+constexpr int kSelUnit = 4096;
+constexpr int kSelCap = 2 * kSelUnit;
+template <int NT, int SEL>
+constexpr int kSelKpt = SEL * kSelUnit / NT;
 
 // MF: Q.K on the matrix cores (model-dtype instances whose query has the model dtype).
-// SEL: the launch selects each head's top k from its bounds itself (segment A only).
-template <int D, int MT, int G, int NT, bool I8, bool MF = false, bool SEL = false>
+// SEL > 0: the launch selects each head's top k from its bounds itself (segment A only), from up
+// to SEL * kSelUnit candidates.
+template <int D, int MT, int G, int NT, bool I8, bool MF = false, int SEL = 0>
 __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   using L = Lanes<D>;
   constexpr int NW = NT / 64;
@@ -755,7 +760,7 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   __shared__ uint32_t s_excl[64];  // segment B: bitmap of excluded blocks in this run
   static_assert(!MF || (!I8 && MT != LKV_F32), "the matrix-core path reads model-dtype pairs");
   __shared__ float s_pb[MF ? NW : 1][MF ? kMfBroadcast<G, kMfMaxPairs> : 1];
-  using SelLds = typename std::conditional<SEL, lkv::SelectLds<NT, kSelKpt<NT>>, char>::type;
+  using SelLds = typename std::conditional<(SEL > 0), lkv::SelectLds<NT, kSelKpt<NT, (SEL > 0 ? SEL : 1)>>, char>::type;
   __shared__ SelLds s_sel;
   using V8 = typename Mfma<MT == LKV_F32 ? LKV_F16 : MT>::V8;
 
@@ -776,10 +781,10 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
   // positions [sel_base, sel_base + run) of the ascending selected list.
   const int32_t* idx_h;
   int sel_base = 0;
-  if constexpr (!SEL) {
+  if constexpr (SEL == 0) {
     idx_h = a.idx + (int64_t)h * a.idx_stride;
   } else {
-    const lkv::SelectPick pk = lkv::block_top_k<NT, kSelKpt<NT>>(a.bounds + (int64_t)h * a.bound_stride, a.bounds_aligned != 0, a.n_cand, a.k, s_sel);
+    const lkv::SelectPick pk = lkv::block_top_k<NT, kSelKpt<NT, SEL>>(a.bounds + (int64_t)h * a.bound_stride, a.bounds_aligned != 0, a.n_cand, a.k, s_sel);
     const int has_sink = a.sink_block >= 0;
     const int first = split * a.per_a;
     const int last = min(a.n_a, first + a.per_a);
@@ -789,7 +794,7 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
     int32_t* out_h = (a.idx_out != nullptr && split == 0) ? a.idx_out + (int64_t)h * a.idx_out_stride : nullptr;
     int pos = pk.pos;
 #pragma unroll
-    for (int u = 0; u < kSelKpt<NT>; ++u) {
+    for (int u = 0; u < kSelKpt<NT, SEL>; ++u) {
       if ((pk.take >> u) & 1u) {
         const int32_t id = pk.i0 + u + a.cand_offset;
         if (pos >= js && pos < je) ids[pos - js] = id;
@@ -846,7 +851,7 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       // A fused-selection instance keeps the pairing of the instance it stands in for, so that both
       // fold each wave's chunks in the same order (with two pairs in flight a wave interleaves their
       // 16-row chunks).
-      constexpr bool HYB = I8 && NT == kThreads && !SEL;
+      constexpr bool HYB = I8 && NT == kThreads && SEL == 0;
       constexpr int NPA = ((I8 && NT == kThreads) || MT == LKV_F32) ? 1 : 2;
       for (int j = js + wave; j < je; j += NPA * NW) {
         const int b0 = idx_h[j - sel_base];
@@ -869,7 +874,7 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
         attend_two<D, MT, G, I8, NPA>(a, a.sel, b0, b1, h, a.bs, q, r, c, st);
       }
     }
-  } else if constexpr (!SEL) {
+  } else if constexpr (SEL == 0) {
     // Segment B: remainder blocks of this run that idx does not name.
     const int sb = split - a.splits_a;
     const int lo = a.rem_first + sb * a.per_b;
@@ -1144,7 +1149,7 @@ Inst pick_instance(const DecodeArgs& a, bool sel) {
   return (D == 128 && G == 4) ? Inst::kGeneral : Inst::kInt8x8;
 }
 
-template <int D, int MT, int G, bool SEL>
+template <int D, int MT, int G, int SEL>
 int launch_inst(hipStream_t stream, DecodeArgs& a, Inst inst) {
   const dim3 grid((a.splits_a + a.splits_b) * a.n_kv);
   bool done = false;
@@ -1154,7 +1159,7 @@ int launch_inst(hipStream_t stream, DecodeArgs& a, Inst inst) {
       done = true;
     }
   }
-  if constexpr (G <= 4 && !SEL) {
+  if constexpr (G <= 4 && SEL == 0) {
     if (inst == Inst::kVector8) {
       hipLaunchKernelGGL((sparse_decode_kernel<D, MT, G, kThreadsHbm, false>), grid, dim3(kThreadsHbm), 0, stream, a);
       done = true;
@@ -1184,7 +1189,9 @@ int launch(hipStream_t stream, DecodeArgs& a) {
   if ((inst == Inst::kMatrix8 && (MT == LKV_F32 || G > 4)) || (inst == Inst::kInt8x8 && (G > 4 || (D == 128 && G == 4))) ||
       (inst == Inst::kVector8 && (G > 4 || sel)))
     inst = Inst::kGeneral;  // no such instance (pick_instance never asks for one)
-  const int rc = sel ? launch_inst<D, MT, G, true>(stream, a, inst) : launch_inst<D, MT, G, false>(stream, a, inst);
+  const int rc = !sel                      ? launch_inst<D, MT, G, 0>(stream, a, inst)
+                 : a.n_cand <= kSelUnit ? launch_inst<D, MT, G, 1>(stream, a, inst)
+                                        : launch_inst<D, MT, G, 2>(stream, a, inst);
   if (rc != LKV_OK) return rc;
   hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(512), 0, stream, a.part_ml, a.part_o, S,
                      a.out, a.out_dtype, a.lse);
@@ -1499,7 +1506,8 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
     LKV_CHECK_ARG(fsel->bounds != nullptr && fsel->n_cand > 0 && d.k <= fsel->n_cand, "selection of k=%d from %d candidates", d.k,
                   fsel->n_cand);
     LKV_CHECK_ARG(!select_in_decode || (fsel->n_cand <= kSelCap && p.per_a <= lkv::kSelBins),
-                  "a selection inside the decode launch takes at most %d candidates and %d items per workgroup", kSelCap, lkv::kSelBins);
+                  "a selection inside the decode launch takes at most %d candidates and %d items per workgroup", kSelCap,
+                  lkv::kSelBins);
     LKV_CHECK_ARG(select_in_decode || fsel->ids != nullptr, "no room for the selected ids");
   }
   if (select_in_decode) {
@@ -1630,11 +1638,11 @@ extern "C" int lkv_sparse_decode_static(uintptr_t stream, const lkv_decode_desc*
 
 // ---- a1 + a2 + a5 + a6: one selecting layer's decode step ---------------------------------------
 // Where the top k is chosen. Inside the decode launch it saves the selection's own launch, but every
-// decode workgroup then waits for its own pass over all of the head's bounds; measured on MI355X,
+// decode workgroup then waits for its own pass over all of the head's bounds. Measured on MI355X,
 // the in-launch selection wins at 2,046 and 4,094 candidates per head (1.5 and 1.9 us per layer at
-// the 32K- and 64K-token 1B shapes) and loses at 8,190 (1.7 us at the 128K-token 8B shape), where
-// the one-workgroup-per-head selection launch is quicker. Up to kFuseMaxCand candidates it selects
-// in the decode launch, beyond it in its own; the results are the same bits either way.
+// the 32K- and 64K-token 1B shapes) and at 8,190 (1.6 us at the 128K-token 8B shape, with 8,192
+// key slots per workgroup). Up to kFuseMaxCand candidates it selects in the decode launch, beyond
+// it in its own (the streaming selection); the results are the same bits either way.
 constexpr int kFuseMaxCand = kSelCap;
 
 extern "C" size_t lkv_select_decode_workspace_bytes(const lkv_decode_desc* desc, int n_cand) {

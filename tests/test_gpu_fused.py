@@ -1,5 +1,5 @@
 """The one-call decode step (lkv_select_decode: the bound kernel, then the top K chosen inside the
-decode launch up to 4,096 candidates per head, or by its own launch beyond) against the
+decode launch up to 8,192 candidates per head, or by its own launch beyond) against the
 two-entry-point path (lkv_bound_topk, then lkv_sparse_decode) and against the oracle: the selected
 ids are identical, the outputs equal bit for bit (the same plan and partials), and both match the
 float64 oracle within the 2e-3 bar (lazykv/selection.py:38-62, lazykv/attention.py:97-136)."""
@@ -49,8 +49,10 @@ CASES = [
     (4, 2, 130, 32, 64, 100, 1, torch.float16, "host"),
     (1, 4, 700, 16, 64, 3, 16, torch.bfloat16, "hbm"),
     (4, 1, 60, 64, 128, 58, 60, torch.float16, "hbm"),  # every candidate selected
-    (2, 4, 4098, 16, 64, 300, 3, torch.bfloat16, "hbm"),  # 4,096 candidates: the most selected inside the decode launch
-    (2, 4, 4099, 16, 64, 300, 3, torch.bfloat16, "hbm"),  # 4,097: the top-K in its own launch
+    (2, 4, 4098, 16, 64, 300, 3, torch.bfloat16, "hbm"),  # 4,096 candidates: the most in 4,096 key slots
+    (2, 4, 4099, 16, 64, 300, 3, torch.bfloat16, "hbm"),  # 4,097: 8,192 key slots
+    (2, 4, 8194, 16, 64, 600, 3, torch.float16, "hbm"),  # 8,192: the most selected inside the decode launch
+    (1, 8, 8195, 16, 64, 600, 3, torch.float16, "hbm"),  # 8,193: the top-K in its own launch
     (1, 8, 20002, 16, 64, 700, 12, torch.float16, "host"),  # 20,000: the streaming top-K
 ]
 
@@ -216,6 +218,8 @@ DESIGNED = [
     ("distinct", 2, 4, 2046, 512),
     ("negative and zero", 2, 4, 3000, 1100),
     ("three values", 1, 8, 4096, 4096),  # every candidate selected
+    ("outlier and a dense cluster", 2, 4, 8000, 2500),  # 8,192 key slots
+    ("distinct", 1, 4, 8190, 512),
 ]
 
 
