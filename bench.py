@@ -806,16 +806,35 @@ def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
     ref_wall = statistics.median(ref_walls)
     nb = n // BS
     P = packed_pair_bytes(BS, d)
+    # The tier build of one layer as a single launch on an otherwise idle GPU (the kernel's own
+    # rate): a layer's float16 K/V in HBM -> int8 records in the mapped host pool + metadata. In the
+    # prefill itself the same work is split into per-chunk launches that overlap the next chunk's
+    # compute, so their summed device time (reported apart) includes the sharing.
+    from lazykv_amd import kernels
+
+    gk = torch.Generator(device=dev).manual_seed(1)
+    kk = torch.randn((1, H, nb * BS, d), device=dev, generator=gk).to(torch.float16)
+    vv = torch.randn((1, H, nb * BS, d), device=dev, generator=gk).to(torch.float16)
+    kmin_i = torch.empty((1, H, nb, d), dtype=torch.float16, device=dev)
+    kmax_i = torch.empty_like(kmin_i)
+    src_i, dst_i = kernels.dense_source(kk, vv, BS), kernels.record_source(pools[0], torch.float16)
+
+    def build_one() -> None:
+        kernels.store_blocks(src_i, dst=dst_i, n_kv=H, head_dim=d, block_size=BS, first_block=0, n_blocks=nb, kmin=kmin_i, kmax=kmax_i)
+
+    build_us = kernel_us([build_one], 5)[0]
+    del kk, vv
     b_read = 2 * H * nb * BS * d * 2  # the layer's float16 K and V
     b_rec = nb * H * P  # int8 records, written to mapped host memory
     b_meta = 2 * H * nb * d * 2
-    pcie = b_rec / (boundary_us * 1e-6) / 1e9
+    pcie = b_rec / (build_us * 1e-6) / 1e9
     t_roof = max((b_read + b_meta) / (HBM_PEAK_GBPS * 1e9), b_rec / (PCIE_PEAK_GBPS * 1e9)) * 1e6
-    log(f"prefill32k: tier build {boundary_us:.1f} us/layer ({pcie:.1f} GB/s of records to host), prefill wall {wall_s:.3f}s vs chunk-major + tier build {ref_wall:.3f}s")
+    log(f"prefill32k: tier build {build_us:.1f} us/layer in one launch ({pcie:.1f} GB/s of records to host); in the prefill, per-chunk launches overlapping "
+        f"compute, {boundary_us:.1f} us/layer of device time; prefill wall {wall_s:.3f}s vs chunk-major + tier build {ref_wall:.3f}s")
     out = {
         "metric": "tiered prefill: int8 tier build µs/layer (fused pack + key min/max, records written to mapped host memory) & achieved PCIe GB/s (% roofline)",
-        "value": round(boundary_us, 2), "unit": "us/layer", "n_gpus": 1, "steps": reps, "warmup": args.warmup,
-        "ms_per_step": round(boundary_us * L / 1e3, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "value": round(build_us, 2), "unit": "us/layer", "n_gpus": 1, "steps": reps, "warmup": args.warmup,
+        "ms_per_step": round(build_us * L / 1e3, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic",
         "config": {"workload": f"Llama-3.2-1B-shaped layer-major prefill: {L} layers (hidden 2048, 32/8 heads, d {d}), {n}-token prompt uniform over 128,256 ids, "
                                f"float16 weights ~N(0,0.02), chunks of {chunk}, every layer's KV into the int8 host tier (dense_layers 0)",
@@ -823,10 +842,13 @@ def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
         "roofline": {"bound": "pcie", "kernel": "store_blocks_kernel (int8 records to host + metadata of the dequantised keys)", "achieved": round(pcie, 2),
                      "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(pcie / PCIE_PEAK_GBPS, 4), "traffic": pmc_traffic().get("prefill/store_blocks_kernel"),
                      "traffic_note": f"calibrated FETCH_SIZE + WRITE_SIZE bytes per launch (K/V read + records and metadata written), algorithmic {b_read + b_rec + b_meta}; source {TRAFFIC_FILE.relative_to(ROOT)}",
-                     "algorithmic_bytes": b_rec, "kernel_us": round(boundary_us, 2),
-                     "hbm_read_bytes": b_read, "hbm_read_gbps": round(b_read / (boundary_us * 1e-6) / 1e9, 1), "metadata_bytes": b_meta},
+                     "algorithmic_bytes": b_rec, "kernel_us": round(build_us, 2),
+                     "hbm_read_bytes": b_read, "hbm_read_gbps": round(b_read / (build_us * 1e-6) / 1e9, 1), "metadata_bytes": b_meta},
         "byte_roofline": {"hbm_bytes_per_layer": b_read + b_meta, "pcie_bytes_per_layer": b_rec, "t_roof_us_at_64gbps": round(t_roof, 2),
-                          "frac_at_64gbps": round(t_roof / boundary_us, 4)},
+                          "frac_at_64gbps": round(t_roof / build_us, 4)},
+        "tier_build_in_prefill": {"device_us_per_layer": round(boundary_us, 2),
+                                  "note": "the same records written by one store_blocks launch per chunk, each overlapping the next chunk's compute on a second stream; "
+                                          "summed device time of those launches, per layer"},
         "prefill": {"wall_s": round(wall_s, 4), "per_layer_ms": round(wall_s / L * 1e3, 3), "chunks": runs[0][2],
                     "chunk_major_then_tier_wall_s": round(ref_wall, 4), "ratio_to_chunk_major": round(wall_s / ref_wall, 4)},
     }
