@@ -134,6 +134,108 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
   }
 }
 
+// ---- the bound on the matrix cores -------------------------------------------------------------
+// When the query has the metadata's dtype, the bounds of 16 blocks for the G query heads of a KV
+// head are two matrix products, sum_d q+_d kmax_d and sum_d q-_d kmin_d (q+ = max(q, 0) and
+// q- = q - q+ are exact in the model dtype): one v_mfma_f32_16x16x32 per 32 channels each, A = the
+// 16 blocks' metadata rows as loaded (lane l: block l % 16, channels 32s + 8 (l / 16) .. + 7), B = q+
+// or q- (lane l: head l % 16, zero past G). Products of two model-dtype values are exact in float32
+// and are summed in float32, as in the vector kernel (in another order). The result (lane l: blocks
+// 4 (l / 16) + i, i < 4, of head l % 16) is maxed over the G heads across each 16-lane row, and the
+// row's first lane writes its 4 bounds. The vector kernel spends ~150 instructions per wave on 4
+// blocks (widening, 16 float32 FMAs per head, DPP row sums); here 16 blocks take 8 MFMAs. Measured
+// in the decode step (A/B, same box): the 8B-shaped HBM step 33.9 -> 33.3 us per layer with 4-wave
+// workgroups of one 16-block tile per wave, the 1B step unchanged (20.5); two or four tiles per
+// wave, or 8- and 16-wave workgroups, were slower at the 1B shape (21.2-22.7).
+#ifndef LKV_BOUND_MF_THREADS
+#define LKV_BOUND_MF_THREADS 256
+#endif
+#ifndef LKV_BOUND_MF_TILES
+#define LKV_BOUND_MF_TILES 1
+#endif
+constexpr int kBoundMfThreads = LKV_BOUND_MF_THREADS;
+constexpr int kBoundMfTiles = LKV_BOUND_MF_TILES;       // 16-block tiles per wave, all loads in flight together
+constexpr int kBoundMfBlocks = kBoundMfThreads / 64 * 16 * kBoundMfTiles;  // blocks per workgroup
+
+typedef __attribute__((ext_vector_type(4))) float bf32x4;
+template <int MT>
+struct BoundMma;
+template <>
+struct BoundMma<LKV_BF16> {
+  typedef __attribute__((ext_vector_type(8))) __bf16 V8;
+  __device__ __forceinline__ static bf32x4 mma(V8 a, V8 b, bf32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+};
+template <>
+struct BoundMma<LKV_F16> {
+  typedef __attribute__((ext_vector_type(8))) _Float16 V8;
+  __device__ __forceinline__ static bf32x4 mma(V8 a, V8 b, bf32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+};
+
+template <int D, int MT, int G>
+__global__ __launch_bounds__(kBoundMfThreads) void bound_kernel_mf(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kmin,
+                                                                   const uint16_t* __restrict__ kmax, int64_t meta_head_stride, int n_kv,
+                                                                   int cand_offset, int n_cand, int rank_mode, float* __restrict__ bounds,
+                                                                   int64_t bound_stride) {
+  using M = BoundMma<MT>;
+  using V8 = typename M::V8;
+  constexpr int NS = D / 32;
+  constexpr int kWaves = kBoundMfThreads / 64;
+  constexpr int T = kBoundMfTiles;
+  static_assert(G <= 16, "one MFMA column per query head");
+  const int h = blockIdx.x % n_kv;
+  const int split = blockIdx.x / n_kv;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int b0 = (split * kWaves + wave) * (16 * T);  // this wave's first block
+  if (b0 >= n_cand) return;                          // wave-uniform; the kernel has no barrier
+  const int64_t base = (int64_t)h * meta_head_stride + (int64_t)cand_offset * D + 8 * grp;
+  // Every metadata load of the wave first. A row past the candidates reads the last candidate's
+  // row instead; its bound is not written.
+  uint4 amax[T][NS], amin[T][NS];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int blk = min(b0 + 16 * t + r16, n_cand - 1);
+    const uint16_t* rmax = kmax + base + (int64_t)blk * D;
+    const uint16_t* rmin = kmin + base + (int64_t)blk * D;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      amax[t][s] = *(const uint4*)(rmax + 32 * s);
+      amin[t][s] = *(const uint4*)(rmin + 32 * s);
+    }
+  }
+  // B: q+ and q- of head r16 (zero past G), split by the sign bit of each 16-bit element.
+  const int j = r16;
+  const uint16_t* qrow = q + ((int64_t)h * G + (j < G ? j : 0)) * D + 8 * grp;
+  V8 qp[NS], qn[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    uint4 x = *(const uint4*)(qrow + 32 * s);
+    if (j >= G) x = make_uint4(0u, 0u, 0u, 0u);
+    const uint4 m = make_uint4(((x.x >> 15) & 0x00010001u) * 0xFFFFu, ((x.y >> 15) & 0x00010001u) * 0xFFFFu,
+                               ((x.z >> 15) & 0x00010001u) * 0xFFFFu, ((x.w >> 15) & 0x00010001u) * 0xFFFFu);
+    qp[s] = __builtin_bit_cast(V8, make_uint4(x.x & ~m.x, x.y & ~m.y, x.z & ~m.z, x.w & ~m.w));
+    qn[s] = __builtin_bit_cast(V8, make_uint4(x.x & m.x, x.y & m.y, x.z & m.z, x.w & m.w));
+  }
+  float* bound_h = bounds + (int64_t)h * bound_stride;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    bf32x4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      a = M::mma(__builtin_bit_cast(V8, amax[t][s]), qp[s], a);
+      b = M::mma(__builtin_bit_cast(V8, amin[t][s]), qn[s], b);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = rank_mode == LKV_RANK_MODEL ? lkv::round_through<MT>(lkv::round_through<MT>(a[i]) + lkv::round_through<MT>(b[i]))
+                                            : a[i] + b[i];
+      v = lkv::row16_max(j < G ? v : -INFINITY);
+      const int blk = b0 + 16 * t + 4 * grp + i;
+      if (r16 == 0 && blk < n_cand) bound_h[blk] = v;
+    }
+  }
+}
+
 // Exclusive prefix sum over the workgroup's threads (ascending thread id). `slots` holds one word
 // per wave and is read after a barrier; the caller separates reuses of `slots` by a barrier.
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* slots, uint32_t* total) {
@@ -603,6 +705,14 @@ template <int D, int MT, int G>
 int launch_bound(hipStream_t stream, const void* q, int q_dtype, const void* kmin, const void* kmax, int64_t mhs, int n_kv,
                  int cand_offset, int n_cand, int rank_mode, float* bounds, int64_t bstride) {
   using T = typename lkv::Elem<MT>::T;
+  // A model-dtype query, and 16-byte aligned rows (the strides are multiples of 128 bytes): the matrix cores.
+  if (q_dtype == MT && (((uintptr_t)q | (uintptr_t)kmin | (uintptr_t)kmax) & 15u) == 0) {
+    const int splits_mf = (n_cand + kBoundMfBlocks - 1) / kBoundMfBlocks;
+    hipLaunchKernelGGL((bound_kernel_mf<D, MT, G>), dim3(splits_mf * n_kv), dim3(kBoundMfThreads), 0, stream, (const uint16_t*)q,
+                       (const uint16_t*)kmin, (const uint16_t*)kmax, mhs, n_kv, cand_offset, n_cand, rank_mode, bounds, bstride);
+    LKV_CHECK_LAUNCH("bound");
+    return LKV_OK;
+  }
   const int splits = (n_cand + kBlocksPerWG - 1) / kBlocksPerWG;
   hipLaunchKernelGGL((bound_kernel<D, MT, G>), dim3(splits * n_kv), dim3(kBoundThreads), 0, stream, q, q_dtype,
                      (const T*)kmin, (const T*)kmax, mhs, n_kv, cand_offset, n_cand, rank_mode, bounds, bstride);
