@@ -181,6 +181,40 @@ def test_top_blocks_selects_the_oracle_set(h: int, n: int, d: int, g: int, k: in
         assert (np.diff(b) <= 0).all()
 
 
+@pytest.mark.parametrize(("d", "g", "dt"), [(128, 4, torch.bfloat16), (64, 4, torch.float16), (128, 8, torch.float16), (64, 1, torch.bfloat16), (128, 2, torch.bfloat16)])
+def test_matrix_core_and_vector_bounds_agree_with_the_oracle(d: int, g: int, dt: torch.dtype) -> None:
+    """A query in the metadata's dtype is scored on the matrix cores, a float32 query (the same
+    values) by the vector kernel: both are the oracle's bound within the float32 accumulation error,
+    in both rank modes, and choose the oracle's set under the near-tie rule."""
+    from lazykv_amd import kernels
+
+    h, n, k = 4, 1500, 200
+    q, kmin, kmax = _meta_case(d * g + n, h, n, 16, d, g, dt)
+    want = R.quest_bound(_f64(q), _f64(kmin), _f64(kmax))
+    err = _abs_err(_f64(q), _f64(kmin), _f64(kmax))
+    full_min = torch.cat([torch.zeros((h, 1, d), dtype=dt), kmin], dim=1)[None].cuda()
+    full_max = torch.cat([torch.zeros((h, 1, d), dtype=dt), kmax], dim=1)[None].cuda()
+    tag = "bf16" if dt == torch.bfloat16 else "f16"
+    for qq in (q.cuda(), q.float().cuda()):  # the matrix cores, then the vector kernel
+        for mode in (kernels._lib.RANK_F32, kernels._lib.RANK_MODEL):
+            bnd = torch.empty((h, n), dtype=torch.float32, device="cuda")
+            kernels.bound_topk(qq, full_min, full_max, 0, cand_offset=1, n_cand=n, out_bound=bnd, rank_mode=mode)
+            got = bnd.cpu().numpy().astype(np.float64)
+            if mode == kernels._lib.RANK_F32:
+                assert np.abs(got - want).max() <= err, (qq.dtype, mode)
+            else:
+                # Each half-sum rounded to the model dtype, then their sum: a half-sum a few float32
+                # ulps away from the oracle's can round one model-dtype ulp the other way, so allow
+                # two ulps of the half-sums' magnitude bound.
+                model = R.quest_bound(_f64(q), _f64(kmin), _f64(kmax), "model", tag)
+                mag = np.abs(_f64(q)).max() * np.maximum(np.abs(_f64(kmin)), np.abs(_f64(kmax))).sum(-1).max()
+                tol = mag * (2.0**-6 if dt == torch.bfloat16 else 2.0**-9)
+                assert np.abs(got - model).max() <= tol, (qq.dtype, mode)
+        idx = kernels.bound_topk(qq, full_min, full_max, k, cand_offset=1, n_cand=n)
+        for j in range(h):
+            assert R.selection_ok(idx[j].cpu().numpy() - 1, want[j], k, abs_err=err)[0], (qq.dtype, j)
+
+
 @pytest.mark.parametrize(("h", "n", "d", "k", "sorted_"), [(8, 12289, 128, 512, False), (4, 40000, 64, 2048, True), (2, 100000, 64, 4096, False), (1, 70000, 128, 17, True)])
 def test_long_context_selection_streams_the_bounds(h: int, n: int, d: int, k: int, sorted_: bool) -> None:
     """More candidates per head than the registers hold: the streaming select gives the oracle's set."""
