@@ -123,6 +123,7 @@ struct RawI8 {
   uint32_t kz[EPL / 2];
   uint32_t vs[NI];  // float16 in the low half
   uint32_t vz[NI];
+  uint32_t sv, svz;  // the chunk's value scale / zero pairs as loaded (finish_raw hands them to the rows)
 };
 
 // Every pair this file reads -- HBM or mapped host memory -- is global memory. Reads through this
@@ -225,25 +226,16 @@ __device__ __forceinline__ void load_raw(const Src& s, int bs, int block, int h,
   // The chunk's value scales and zeros in one 64-byte read per row group, as float16 pairs: with
   // 16-lane rows, lane c < 8 loads the pair vs[t0 + 2c, +1] and lane c >= 8 the pair vz[t0 + 2(c - 8), +1];
   // with 8-lane rows, lane c loads both vs[t0 + 2c, +1] and vz[t0 + 2c, +1]. Pairs past the record's bs
-  // rows are not read. Each row's pair is then taken from the lane of its group that holds it.
+  // rows are read as the record's last pair instead (unconditionally: a load under a branch made the
+  // compiler wait for it there); they belong to rows past the block, which are masked. finish_raw
+  // then takes each row's pair from the lane of its group that holds it.
   const int m = L::LPR == 16 ? (c & 7) : c;
-  const bool in_rec = t0 + 2 * m + 2 <= bs;
-  const uint32_t sv = in_rec ? *(const uint32_t*)(scales + 2 * D + (L::LPR == 16 ? (c >> 3) * bs : 0) + t0 + 2 * m) : 0u;
-  const uint32_t svz = (L::LPR == 8 && in_rec) ? *(const uint32_t*)(scales + 2 * D + bs + t0 + 2 * m) : sv;
-  const int base = r * L::LPR;  // first lane of this row group
-  uint32_t wvs[L::NI], wvz[L::NI];
-#pragma unroll
-  for (int i = 0; i < L::NI; ++i) {  // every lane takes part in the shuffles
-    const int local = r + L::RG * i;
-    wvs[i] = (uint32_t)__shfl((int)sv, base + (local >> 1));
-    wvz[i] = (uint32_t)__shfl((int)svz, base + (L::LPR == 16 ? 8 : 0) + (local >> 1));
-  }
+  const int pidx = min(t0 + 2 * m, bs - 2);
+  raw.sv = *gmem<uint32_t>(scales + 2 * D + (L::LPR == 16 ? (c >> 3) * bs : 0) + pidx);
+  raw.svz = L::LPR == 8 ? *gmem<uint32_t>(scales + 2 * D + bs + pidx) : raw.sv;
 #pragma unroll
   for (int i = 0; i < L::NI; ++i) {
     const int row = t0 + r + L::RG * i;
-    // Rows past `limit` are masked before their values are used.
-    raw.vs[i] = (row & 1) ? wvs[i] >> 16 : wvs[i] & 0xffffu;
-    raw.vz[i] = (row & 1) ? wvz[i] >> 16 : wvz[i] & 0xffffu;
     // Branch-free as for model-dtype rows: a masked row reads row 0 of the record, and its
     // consumers mask it.
     const bool ok = i < nit && row < limit;
@@ -252,6 +244,32 @@ __device__ __forceinline__ void load_raw(const Src& s, int bs, int block, int h,
     load_words(rec + bs * D + at, raw.v[i]);
   }
 }
+
+// The second half of an int8 chunk's load: the lane shuffles that hand each row its value scale and
+// zero. Kept apart from the loads so that a wave issues every load of its pairs -- scales and rows --
+// before the first shuffle waits for a scale: with the shuffles between one pair's loads and the
+// next pair's, the pairs of a round arrived one memory latency apart.
+template <int D>
+__device__ __forceinline__ void finish_raw(int t0, int r, RawI8<D>& raw) {
+  using L = Lanes<D>;
+  const int base = r * L::LPR;  // first lane of this row group
+  uint32_t wvs[L::NI], wvz[L::NI];
+#pragma unroll
+  for (int i = 0; i < L::NI; ++i) {  // every lane takes part in the shuffles
+    const int local = r + L::RG * i;
+    wvs[i] = (uint32_t)__shfl((int)raw.sv, base + (local >> 1));
+    wvz[i] = (uint32_t)__shfl((int)raw.svz, base + (L::LPR == 16 ? 8 : 0) + (local >> 1));
+  }
+#pragma unroll
+  for (int i = 0; i < L::NI; ++i) {
+    const int row = t0 + r + L::RG * i;
+    // Rows past `limit` are masked before their values are used.
+    raw.vs[i] = (row & 1) ? wvs[i] >> 16 : wvs[i] & 0xffffu;
+    raw.vz[i] = (row & 1) ? wvz[i] >> 16 : wvz[i] & 0xffffu;
+  }
+}
+template <int D, int MT>
+__device__ __forceinline__ void finish_raw(int, int, RawModel<D, MT>&) {}
 
 // Per-row widening of a raw chunk: key row i / value row i of this lane's channels, as float.
 template <int D, int MT>
@@ -408,11 +426,16 @@ __device__ __forceinline__ void process_two(const DecodeArgs& a, const Src& s, i
       Raw rb;
       load_pair_raw<D, MT>(s, a.bs, ok_a, block_a, h, t0, nit, limit, r, c, ra);
       load_pair_raw<D, MT>(s, a.bs, ok_b, block_b, h, t0, nit, limit, r, c, rb);
+      if (ok_a) finish_raw(t0, r, ra);  // wave-uniform branches: every lane shuffles
+      if (ok_b) finish_raw(t0, r, rb);
       if (ok_a) consume_chunk<D, G>(q, Wd(ra), ra, t0, nit, limit, r, st);
       if (ok_b) consume_chunk<D, G>(q, Wd(rb), rb, t0, nit, limit, r, st);
     } else {
       load_pair_raw<D, MT>(s, a.bs, ok_a, block_a, h, t0, nit, limit, r, c, ra);
-      if (ok_a) consume_chunk<D, G>(q, Wd(ra), ra, t0, nit, limit, r, st);
+      if (ok_a) {
+        finish_raw(t0, r, ra);
+        consume_chunk<D, G>(q, Wd(ra), ra, t0, nit, limit, r, st);
+      }
     }
   }
 }
@@ -710,6 +733,7 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
     const int nit = min(Lanes<D>::NI, (a.bs - t0 + Lanes<D>::RG - 1) / Lanes<D>::RG);
     RawI8<D> raw;
     load_raw<D>(a.sel, a.bs, block, h, t0, nit, a.bs, r, c, raw);
+    finish_raw(t0, r, raw);
     const WidenI8<D, MT> wd(raw);
 #pragma unroll
     for (int i = 0; i < L::NI; ++i) {
