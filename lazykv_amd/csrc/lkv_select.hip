@@ -138,15 +138,18 @@ __global__ __launch_bounds__(kBoundThreads) void bound_kernel(const void* __rest
 // When the query has the metadata's dtype, the bounds of 16 blocks for the G query heads of a KV
 // head are two matrix products, sum_d q+_d kmax_d and sum_d q-_d kmin_d (q+ = max(q, 0) and
 // q- = q - q+ are exact in the model dtype): one v_mfma_f32_16x16x32 per 32 channels each, A = the
-// 16 blocks' metadata rows as loaded (lane l: block l % 16, channels 32s + 8 (l / 16) .. + 7), B = q+
-// or q- (lane l: head l % 16, zero past G). Products of two model-dtype values are exact in float32
-// and are summed in float32, as in the vector kernel (in another order). The result (lane l: blocks
-// 4 (l / 16) + i, i < 4, of head l % 16) is maxed over the G heads across each 16-lane row, and the
-// row's first lane writes its 4 bounds. The vector kernel spends ~150 instructions per wave on 4
-// blocks (widening, 16 float32 FMAs per head, DPP row sums); here 16 blocks take 8 MFMAs. Measured
-// in the decode step (A/B, same box): the 8B-shaped HBM step 33.9 -> 33.3 us per layer with 4-wave
+// 16 blocks' metadata rows (lane l: block l % 16, channels 32s + 8 (l / 16) .. + 7), B = q+ or q-
+// (lane l: head l % 16). Products of two model-dtype values are exact in float32 and are summed in
+// float32, as in the vector kernel (in another order). The result (lane l: blocks 4 (l / 16) + i,
+// i < 4, of head l % 16) is maxed over the G heads across each 16-lane row, and the row's first
+// lane writes its 4 bounds. The vector kernel spends ~150 instructions per wave on 4 blocks
+// (widening, 16 float32 FMAs per head, DPP row sums); here 16 blocks take 8 MFMAs. Measured in the
+// decode step (A/B, same box): the 8B-shaped HBM step 33.9 -> 33.3 us per layer with 4-wave
 // workgroups of one 16-block tile per wave, the 1B step unchanged (20.5); two or four tiles per
-// wave, or 8- and 16-wave workgroups, were slower at the 1B shape (21.2-22.7).
+// wave, or 8- and 16-wave workgroups, were slower at the 1B shape (21.2-22.7). Loading A directly
+// in the matrix-core layout puts 16 rows, 16 bytes each, under every quarter-wave of a load; loading
+// the tile with contiguous 1 KiB loads and transposing it through LDS took the 8B-shaped step from
+// 33.2 to 32.0 us per layer (int8_64k 30.4 -> 30.0, the 1B step 20.3 -> 20.2).
 #ifndef LKV_BOUND_MF_THREADS
 #define LKV_BOUND_MF_THREADS 256
 #endif
@@ -188,33 +191,63 @@ __global__ __launch_bounds__(kBoundMfThreads) void bound_kernel_mf(const uint16_
   const int r16 = lane & 15, grp = lane >> 4;
   const int b0 = (split * kWaves + wave) * (16 * T);  // this wave's first block
   if (b0 >= n_cand) return;                          // wave-uniform; the kernel has no barrier
-  const int64_t base = (int64_t)h * meta_head_stride + (int64_t)cand_offset * D + 8 * grp;
-  // Every metadata load of the wave first. A row past the candidates reads the last candidate's
-  // row instead; its bound is not written.
-  uint4 amax[T][NS], amin[T][NS];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const int blk = min(b0 + 16 * t + r16, n_cand - 1);
-    const uint16_t* rmax = kmax + base + (int64_t)blk * D;
-    const uint16_t* rmin = kmin + base + (int64_t)blk * D;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      amax[t][s] = *(const uint4*)(rmax + 32 * s);
-      amin[t][s] = *(const uint4*)(rmin + 32 * s);
-    }
-  }
-  // B: q+ and q- of head r16 (zero past G), split by the sign bit of each 16-bit element.
+  // B: q+ and q- of head r16, split by the sign bit of each 16-bit element. Columns r16 >= G hold
+  // head 0's query; their results are masked before the maximum over heads.
   const int j = r16;
   const uint16_t* qrow = q + ((int64_t)h * G + (j < G ? j : 0)) * D + 8 * grp;
   V8 qp[NS], qn[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    uint4 x = *(const uint4*)(qrow + 32 * s);
-    if (j >= G) x = make_uint4(0u, 0u, 0u, 0u);
+    const uint4 x = *(const uint4*)(qrow + 32 * s);
     const uint4 m = make_uint4(((x.x >> 15) & 0x00010001u) * 0xFFFFu, ((x.y >> 15) & 0x00010001u) * 0xFFFFu,
                                ((x.z >> 15) & 0x00010001u) * 0xFFFFu, ((x.w >> 15) & 0x00010001u) * 0xFFFFu);
     qp[s] = __builtin_bit_cast(V8, make_uint4(x.x & ~m.x, x.y & ~m.y, x.z & ~m.z, x.w & ~m.w));
     qn[s] = __builtin_bit_cast(V8, make_uint4(x.x & m.x, x.y & m.y, x.z & m.z, x.w & m.w));
+  }
+  // Each wave's 16 x D tile of kmax and of kmin is read with coalesced loads (load s, lane l: the
+  // 16 bytes at 1024 s + 16 l of the tile) and handed to the matrix-core layout through the wave's
+  // own LDS (lane l: block l % 16, channels 32 s + 8 (l / 16) .. + 7). A row past the candidates
+  // reads the last candidate's row instead; its bound is not written. LDS holds 16-byte chunk k of
+  // row r at r * D / 8 + (k ^ swz(r)), so that a store of a row and a read of one chunk of 16 rows
+  // each touch 64 distinct banks.
+  constexpr int kChunks = D / 8;  // 16-byte chunks per row
+  constexpr int kRowsPerLoad = 64 / kChunks;
+  static_assert(NS * kRowsPerLoad == 16, "NS loads of 64 lanes cover the 16-row tile");
+  __shared__ __align__(16) uint4 s_tile[kWaves][T][2][16 * kChunks];
+  const int64_t base = (int64_t)h * meta_head_stride + (int64_t)cand_offset * D;
+  const auto swz = [](int r) { return kChunks == 16 ? r : (r >> 1) & (kChunks - 1); };
+  uint4 amax[T][NS], amin[T][NS];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int r = kRowsPerLoad * s + lane / kChunks, k = lane % kChunks;
+      const int64_t off = base + (int64_t)min(b0 + 16 * t + r, n_cand - 1) * D + 8 * k;
+      amax[t][s] = *(const uint4*)(kmax + off);
+      amin[t][s] = *(const uint4*)(kmin + off);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int r = kRowsPerLoad * s + lane / kChunks, k = lane % kChunks;
+      s_tile[wave][t][0][r * kChunks + (k ^ swz(r))] = amax[t][s];
+      s_tile[wave][t][1][r * kChunks + (k ^ swz(r))] = amin[t][s];
+    }
+  }
+  // The tile is this wave's alone: the wave's LDS stores complete before its reads in issue order.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int k = 4 * s + grp;
+      amax[t][s] = s_tile[wave][t][0][r16 * kChunks + (k ^ swz(r16))];
+      amin[t][s] = s_tile[wave][t][1][r16 * kChunks + (k ^ swz(r16))];
+    }
   }
   float* bound_h = bounds + (int64_t)h * bound_stride;
 #pragma unroll
