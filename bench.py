@@ -206,6 +206,24 @@ def dma_h2d_gbps(host, reps: int = 3) -> float:  # noqa: ANN001
     return src.numel() * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
 
+def dma_d2h_gbps(host, reps: int = 3) -> float:  # noqa: ANN001
+    """The copy engines' device-to-host rate into the same pinned pool (a plain hipMemcpyAsync):
+    the link's practical write ceiling, to set the kernels' writes to host memory beside."""
+    import torch
+
+    dst = host.reshape(-1).view(torch.uint8)[: 512 << 20]
+    src = torch.zeros_like(dst, device="cuda")
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src, non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize()
+    return dst.numel() * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
 def _pmc_file() -> dict:
     try:
         with open(TRAFFIC_FILE) as f:
@@ -829,7 +847,11 @@ def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
     b_meta = 2 * H * nb * d * 2
     pcie = b_rec / (build_us * 1e-6) / 1e9
     t_roof = max((b_read + b_meta) / (HBM_PEAK_GBPS * 1e9), b_rec / (PCIE_PEAK_GBPS * 1e9)) * 1e6
-    log(f"prefill32k: tier build {build_us:.1f} us/layer in one launch ({pcie:.1f} GB/s of records to host); in the prefill, per-chunk launches overlapping "
+    # The link's write ceiling: the copy engines writing 512 MiB into the first layer's host pool
+    # (the pool is rewritten by every later prefill, so the probe's zeros do not matter).
+    write_ceiling = dma_d2h_gbps(pools[0])
+    log(f"prefill32k: tier build {build_us:.1f} us/layer in one launch ({pcie:.1f} GB/s of records to host, {pcie / write_ceiling:.3f} of the copy engines' "
+        f"{write_ceiling:.1f} GB/s); in the prefill, per-chunk launches overlapping "
         f"compute, {boundary_us:.1f} us/layer of device time; prefill wall {wall_s:.3f}s vs chunk-major + tier build {ref_wall:.3f}s")
     out = {
         "metric": "tiered prefill: int8 tier build µs/layer (fused pack + key min/max, records written to mapped host memory) & achieved PCIe GB/s (% roofline)",
@@ -843,7 +865,8 @@ def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
                      "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(pcie / PCIE_PEAK_GBPS, 4), "traffic": pmc_traffic().get("prefill/store_blocks_kernel"),
                      "traffic_note": f"calibrated FETCH_SIZE + WRITE_SIZE bytes per launch (K/V read + records and metadata written), algorithmic {b_read + b_rec + b_meta}; source {TRAFFIC_FILE.relative_to(ROOT)}",
                      "algorithmic_bytes": b_rec, "kernel_us": round(build_us, 2),
-                     "hbm_read_bytes": b_read, "hbm_read_gbps": round(b_read / (build_us * 1e-6) / 1e9, 1), "metadata_bytes": b_meta},
+                     "hbm_read_bytes": b_read, "hbm_read_gbps": round(b_read / (build_us * 1e-6) / 1e9, 1), "metadata_bytes": b_meta,
+                     "link_write_ceiling_gbps": round(write_ceiling, 2), "frac_of_link_write_ceiling": round(pcie / write_ceiling, 4)},
         "byte_roofline": {"hbm_bytes_per_layer": b_read + b_meta, "pcie_bytes_per_layer": b_rec, "t_roof_us_at_64gbps": round(t_roof, 2),
                           "frac_at_64gbps": round(t_roof / build_us, 4)},
         "tier_build_in_prefill": {"device_us_per_layer": round(boundary_us, 2),
