@@ -215,6 +215,25 @@ def test_matrix_core_and_vector_bounds_agree_with_the_oracle(d: int, g: int, dt:
             assert R.selection_ok(idx[j].cpu().numpy() - 1, want[j], k, abs_err=err)[0], (qq.dtype, j)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n", [1, 7, 16, 17, 63, 64, 65, 129])
+def test_matrix_core_bound_on_partial_tiles(n: int, d: int) -> None:
+    """Candidate counts around the matrix-core kernel's 16-block tiles and 64-block workgroups: a
+    tile past the last candidate reads that candidate's row and writes nothing, so every bound is
+    the oracle's and the words after the last row keep their sentinel."""
+    from lazykv_amd import kernels
+
+    h, g, dt = 3, 4, torch.bfloat16
+    q, kmin, kmax = _meta_case(1000 * d + n, h, n, 16, d, g, dt)
+    want = R.quest_bound(_f64(q), _f64(kmin), _f64(kmax))
+    err = _abs_err(_f64(q), _f64(kmin), _f64(kmax))
+    flat = torch.full((h * n + 64,), -7.0, dtype=torch.float32, device="cuda")
+    kernels.bound_topk(q.cuda(), kmin[None].cuda(), kmax[None].cuda(), 0, n_cand=n, out_bound=flat[: h * n].view(h, n), rank_mode=kernels._lib.RANK_F32)
+    got = flat.cpu().numpy().astype(np.float64)
+    assert np.abs(got[: h * n].reshape(h, n) - want).max() <= err
+    assert (got[h * n :] == -7.0).all()
+
+
 @pytest.mark.parametrize(("h", "n", "d", "k", "sorted_"), [(8, 12289, 128, 512, False), (4, 40000, 64, 2048, True), (2, 100000, 64, 4096, False), (1, 70000, 128, 17, True)])
 def test_long_context_selection_streams_the_bounds(h: int, n: int, d: int, k: int, sorted_: bool) -> None:
     """More candidates per head than the registers hold: the streaming select gives the oracle's set."""
