@@ -189,6 +189,24 @@ int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void*
                       const lkv_kv_source* sink, const lkv_kv_source* cur, void* out, int out_dtype, float* lse,
                       void* ws, size_t ws_bytes);
 
+/* ---- a1 + a2 + f3 + a6: one selecting layer's hybrid decode step
+ * (lazykv/tiered.py:383-387 rank + :389-487 the hybrid fetch + lazykv/attention.py:97-136 attend;
+ * the top_blocks rule of lazykv/selection.py:56-62). lkv_bound_topk followed by
+ * lkv_hybrid_decode in one call: the bound kernel scores candidates cand_offset ..
+ * cand_offset+n_cand-1 into the workspace, and the launch that updates the residency tables
+ * first chooses each head's top desc->k itself (up to 8,192 candidates per head; beyond, the
+ * selection takes a launch of its own), so the step is four launches instead of five. The ids,
+ * the tables after the call, the output and the LSE equal lkv_bound_topk followed by
+ * lkv_hybrid_decode, bit for bit. out_idx, if not NULL, receives the selected ids in ascending
+ * order (idx_stride apart per head). Arguments as in those two calls. */
+size_t lkv_select_hybrid_decode_workspace_bytes(const lkv_decode_desc* desc, int n_cand);
+int lkv_select_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype, const void* kmin,
+                             const void* kmax, int meta_dtype, int64_t meta_head_stride, int cand_offset, int n_cand,
+                             int rank_mode, const lkv_kv_source* host, const lkv_kv_source* slots, int32_t* block_slot,
+                             int64_t block_slot_stride, int32_t* slot_block, int64_t slot_block_stride,
+                             const lkv_kv_source* sink, const lkv_kv_source* cur, void* out, int out_dtype, float* lse,
+                             int32_t* out_idx, int64_t idx_stride, void* ws, size_t ws_bytes);
+
 /* ---- a8: exact two-partial merge (lazykv/exact.py:69-85 merge_lse)
  * rows x d outputs (dtype_in) and their LSEs; an empty partial (lse -inf) contributes 0.
  * out/lse may alias out_a/lse_a. */

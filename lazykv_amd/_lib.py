@@ -106,6 +106,12 @@ SIGNATURES: dict[str, tuple] = {
         [_U, ctypes.POINTER(DecodeDesc), _P, _I, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I64, _P, _I64, _P, _I64,
          ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I, _P, _P, _SZ],
     ),
+    "lkv_select_hybrid_decode_workspace_bytes": (_SZ, [ctypes.POINTER(DecodeDesc), _I]),
+    "lkv_select_hybrid_decode": (
+        _I,
+        [_U, ctypes.POINTER(DecodeDesc), _P, _I, _P, _P, _I, _I64, _I, _I, _I, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource),
+         _P, _I64, _P, _I64, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I, _P, _P, _I64, _P, _SZ],
+    ),
     "lkv_merge_lse": (_I, [_U, _P, _P, _P, _P, _I, _I64, _I, _P, _I, _P]),
     "lkv_store_blocks": (_I, [_U, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _I, _I, _I, _I, _I, _P, _P, _I, _I64]),
     "lkv_pack_int8": (_I, [_U, _P, _I, _I64, _I, _I, _P]),

@@ -1262,15 +1262,49 @@ __device__ __forceinline__ uint32_t res_block_scan(uint32_t v, uint32_t* slots, 
   return before + x - v;
 }
 
+// The selection a residency launch makes first (SEL): the k highest of the head's n_cand bounds,
+// by lkv_bound_topk's rule, written ascending to `ids` for the decode launch.
+struct ResSelect {
+  const float* bounds;
+  int64_t bound_stride;
+  int n_cand, cand_offset;
+  int aligned;  // rows padded to a multiple of 4 floats, 16-byte aligned
+  int32_t* ids;
+  int64_t ids_stride;
+};
+constexpr int kResSelKpt = kSelCap / kResThreads;  // candidates per thread of a selecting residency launch
+
+template <bool SEL>
 __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int k,
                                                                 int32_t* __restrict__ block_slot, int64_t bslot_stride,
                                                                 int64_t n_blocks, int32_t* __restrict__ slot_block,
                                                                 int64_t sblock_stride, int32_t* __restrict__ loc,
-                                                                int64_t loc_stride) {
+                                                                int64_t loc_stride, ResSelect rs) {
   __shared__ uint32_t hit[kMaxSlots / 32];
   __shared__ int32_t victims[kMaxSlots];
   __shared__ uint32_t scan_a[kResThreads / 64], scan_b[kResThreads / 64];
+  using SelLds = typename std::conditional<SEL, lkv::SelectLds<kResThreads, kResSelKpt>, char>::type;
+  __shared__ SelLds s_sel;
+  __shared__ int32_t s_ids[SEL ? kMaxSlots : 1];
   const int h = blockIdx.x;
+  if constexpr (SEL) {
+    // The head's top k, ascending, into LDS for the residency pass and to `ids` for the decode.
+    const lkv::SelectPick pk = lkv::block_top_k<kResThreads, kResSelKpt>(rs.bounds + (int64_t)h * rs.bound_stride, rs.aligned != 0, rs.n_cand, k, s_sel);
+    int32_t* ids_h = rs.ids + (int64_t)h * rs.ids_stride;
+    int pos = pk.pos;
+#pragma unroll
+    for (int u = 0; u < kResSelKpt; ++u) {
+      if ((pk.take >> u) & 1u) {
+        const int32_t id = pk.i0 + u + rs.cand_offset;
+        if (pos < k) {
+          s_ids[pos] = id;
+          ids_h[pos] = id;
+        }
+        ++pos;
+      }
+    }
+    __syncthreads();
+  }
   const int n_slots = k;
   const int per = (k + kResThreads - 1) / kResThreads;  // <= kResPer
   const int i0 = threadIdx.x * per;
@@ -1283,7 +1317,7 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
 #pragma unroll
   for (int u = 0; u < kResPer; ++u) {
     const int i = i0 + u;
-    blk[u] = (u < per && i < k) ? idx_h[i] : -1;
+    blk[u] = (u < per && i < k) ? (SEL ? s_ids[i] : idx_h[i]) : -1;
     const bool valid = blk[u] >= 0 && (int64_t)blk[u] < n_blocks;
     cur[u] = valid ? bslot_h[blk[u]] : -2;  // -2: not a block of the pool; -1: not resident
     if (valid && (cur[u] < 0 || cur[u] >= n_slots)) cur[u] = -1;  // an entry that names no slot: not resident
@@ -1417,6 +1451,8 @@ struct FusedSelect {
   // false: the top k is chosen by its own launch into `ids` (idx_out, or workspace), and the decode
   // launch reads them, as after lkv_bound_topk
   bool in_decode;
+  // A hybrid call: the residency launch chooses the top k into `ids` itself (no launch of its own)
+  bool in_residency;
   int32_t* ids;
   int64_t ids_stride;
 };
@@ -1526,7 +1562,10 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
   if (slots) a.slots = to_src(slots);
   const bool select_in_decode = fsel != nullptr && fsel->in_decode;
   if (fsel != nullptr) {
-    LKV_CHECK_ARG(attend_sel && !has_rem && res == nullptr, "a fused selection attends a selection, with no remainder and no residency");
+    LKV_CHECK_ARG(attend_sel && !has_rem, "a fused selection attends a selection, with no remainder");
+    LKV_CHECK_ARG(res == nullptr || !fsel->in_decode, "a hybrid call selects before its residency launch");
+    LKV_CHECK_ARG(!fsel->in_residency || (res != nullptr && fsel->n_cand <= kSelCap && d.k <= kMaxSlots),
+                  "a selection inside the residency launch takes at most %d candidates", kSelCap);
     LKV_CHECK_ARG(fsel->bounds != nullptr && fsel->n_cand > 0 && d.k <= fsel->n_cand, "selection of k=%d from %d candidates", d.k,
                   fsel->n_cand);
     LKV_CHECK_ARG(!select_in_decode || (fsel->n_cand <= kSelCap && p.per_a <= lkv::kSelBins),
@@ -1549,7 +1588,10 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
     int rc = lkv_launch_bounds(s, q, q_dtype, fsel->kmin, fsel->kmax, fsel->meta_dtype, fsel->meta_head_stride, d.n_kv,
                                d.n_q / d.n_kv, d.head_dim, fsel->cand_offset, fsel->n_cand, fsel->rank_mode, fsel->bounds,
                                fsel->stride);
-    if (rc == LKV_OK && !select_in_decode) {
+    if (rc == LKV_OK && !select_in_decode && fsel->in_residency) {
+      a.idx = fsel->ids;
+      a.idx_stride = fsel->ids_stride;
+    } else if (rc == LKV_OK && !select_in_decode) {
       rc = lkv_launch_select(s, fsel->bounds, fsel->stride, d.n_kv, fsel->n_cand, d.k, fsel->cand_offset, fsel->ids,
                              fsel->ids_stride);
       a.idx = fsel->ids;
@@ -1558,8 +1600,16 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
     if (rc != LKV_OK) return rc;
   }
   if (res) {  // every argument is checked: update the residency tables, then attend
-    hipLaunchKernelGGL(residency_kernel, dim3(d.n_kv), dim3(kResThreads), 0, s, idx, idx_stride, d.k, res->block_slot,
-                       res->block_slot_stride, sel->n_blocks, res->slot_block, res->slot_block_stride, loc, loc_stride);
+    if (fsel != nullptr && fsel->in_residency) {
+      const ResSelect rs{fsel->bounds, fsel->stride, fsel->n_cand, fsel->cand_offset, fsel->aligned ? 1 : 0, fsel->ids, fsel->ids_stride};
+      hipLaunchKernelGGL(residency_kernel<true>, dim3(d.n_kv), dim3(kResThreads), 0, s, fsel->ids, fsel->ids_stride, d.k,
+                         res->block_slot, res->block_slot_stride, sel->n_blocks, res->slot_block, res->slot_block_stride, loc,
+                         loc_stride, rs);
+    } else {
+      hipLaunchKernelGGL(residency_kernel<false>, dim3(d.n_kv), dim3(kResThreads), 0, s, a.idx, a.idx_stride, d.k,
+                         res->block_slot, res->block_slot_stride, sel->n_blocks, res->slot_block, res->slot_block_stride, loc,
+                         loc_stride, ResSelect{});
+    }
     LKV_CHECK_LAUNCH("residency");
   }
 
@@ -1587,17 +1637,15 @@ extern "C" size_t lkv_hybrid_decode_workspace_bytes(const lkv_decode_desc* d) {
   return base + lkv_align_up((size_t)d->n_kv * (size_t)(d->k > 0 ? d->k : 0) * 4, 256);
 }
 
-extern "C" int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
-                                 const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* idx,
-                                 int64_t idx_stride, int32_t* block_slot, int64_t block_slot_stride, int32_t* slot_block,
-                                 int64_t slot_block_stride, const lkv_kv_source* sink, const lkv_kv_source* cur,
-                                 void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes) {
-  LKV_CHECK_ARG(desc != nullptr && host != nullptr && slots != nullptr && idx != nullptr, "NULL argument");
-  const lkv_decode_desc& d = *desc;
+// What a hybrid call adds to a decode call: a host pool, an HBM slot per selected block, and the
+// tables of which block each slot holds.
+static int check_hybrid(const lkv_decode_desc& d, const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* block_slot,
+                        int64_t block_slot_stride, const int32_t* slot_block, int64_t slot_block_stride) {
+  LKV_CHECK_ARG(host != nullptr && slots != nullptr, "NULL argument");
   LKV_CHECK_ARG(d.attend_selected && d.k > 0, "hybrid decode attends a selection: k > 0 and attend_selected");
   LKV_CHECK_ARG(d.rem_last == d.rem_first, "hybrid decode has no remainder");
   LKV_CHECK_ARG(d.k <= kMaxSlots, "k=%d exceeds the hybrid slot limit %d", d.k, kMaxSlots);
-  LKV_CHECK_ARG(d.n_kv > 0 && idx_stride >= d.k, "bad n_kv or idx_stride");
+  LKV_CHECK_ARG(d.n_kv > 0, "bad n_kv");
   const int model = host->dtype == LKV_INT8_RECORD ? host->deq_dtype : host->dtype;
   LKV_CHECK_ARG(host->dtype == LKV_INT8_RECORD || (lkv_is_model_dtype(host->dtype) && host->v != nullptr),
                 "the hybrid host pool holds model-dtype pairs or int8 records");
@@ -1606,6 +1654,19 @@ extern "C" int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, 
   LKV_CHECK_ARG(slots->n_blocks == d.k, "the slot pool holds k=%d slots per head, got %lld", d.k, (long long)slots->n_blocks);
   LKV_CHECK_ARG(block_slot != nullptr && slot_block != nullptr, "residency tables missing");
   LKV_CHECK_ARG(block_slot_stride >= host->n_blocks && slot_block_stride >= d.k, "residency table strides too small");
+  return LKV_OK;
+}
+
+extern "C" int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
+                                 const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* idx,
+                                 int64_t idx_stride, int32_t* block_slot, int64_t block_slot_stride, int32_t* slot_block,
+                                 int64_t slot_block_stride, const lkv_kv_source* sink, const lkv_kv_source* cur,
+                                 void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes) {
+  LKV_CHECK_ARG(desc != nullptr && host != nullptr && slots != nullptr && idx != nullptr, "NULL argument");
+  const lkv_decode_desc& d = *desc;
+  const int rc = check_hybrid(d, host, slots, block_slot, block_slot_stride, slot_block, slot_block_stride);
+  if (rc != LKV_OK) return rc;
+  LKV_CHECK_ARG(idx_stride >= d.k, "bad idx_stride");
   const size_t need = lkv_hybrid_decode_workspace_bytes(desc);
   LKV_CHECK_ARG(ws != nullptr && ws_bytes >= need, "workspace of %zu bytes needed, got %zu", need, ws_bytes);
   const size_t dec_bytes = lkv_sparse_decode_workspace_bytes(desc);
@@ -1724,4 +1785,72 @@ extern "C" int lkv_select_decode(uintptr_t stream, const lkv_decode_desc* desc, 
   }
   return sparse_decode_impl(stream, desc, q, q_dtype, sel, nullptr, 0, sink, cur, nullptr, out, out_dtype, lse, ws, dec, nullptr,
                             nullptr, 0, nullptr, &fs);
+}
+
+// ---- a1 + a2 + f3 + a6: one selecting layer's hybrid decode step --------------------------------
+// The bound launch, then the residency launch choosing each head's top k itself (one workgroup per
+// head, as the selection's own launch would use) before it updates the tables, then the decode
+// and merge launches of lkv_hybrid_decode: four launches instead of five. Beyond kSelCap
+// candidates the selection takes its own launch. The ids, tables and output are those of
+// lkv_bound_topk followed by lkv_hybrid_decode.
+extern "C" size_t lkv_select_hybrid_decode_workspace_bytes(const lkv_decode_desc* desc, int n_cand) {
+  const size_t base = lkv_hybrid_decode_workspace_bytes(desc);
+  if (base == 0 || n_cand <= 0) return 0;
+  // partials | residency locations | bounds | the selected ids
+  return base + lkv_align_up((size_t)desc->n_kv * lkv_align_up((size_t)n_cand, 4) * 4, 256) +
+         lkv_align_up((size_t)desc->n_kv * (size_t)(desc->k > 0 ? desc->k : 0) * 4, 256);
+}
+
+extern "C" int lkv_select_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype, const void* kmin,
+                                        const void* kmax, int meta_dtype, int64_t meta_head_stride, int cand_offset, int n_cand,
+                                        int rank_mode, const lkv_kv_source* host, const lkv_kv_source* slots, int32_t* block_slot,
+                                        int64_t block_slot_stride, int32_t* slot_block, int64_t slot_block_stride,
+                                        const lkv_kv_source* sink, const lkv_kv_source* cur, void* out, int out_dtype, float* lse,
+                                        int32_t* out_idx, int64_t idx_stride, void* ws, size_t ws_bytes) {
+  LKV_CHECK_ARG(desc != nullptr && q != nullptr && kmin != nullptr && kmax != nullptr, "NULL argument");
+  const lkv_decode_desc& d = *desc;
+  LKV_CHECK_ARG(d.head_dim == 64 || d.head_dim == 128, "head_dim %d unsupported (64 or 128)", d.head_dim);
+  LKV_CHECK_ARG(d.n_kv > 0 && d.n_q > 0 && d.n_q % d.n_kv == 0, "n_q=%d must be a positive multiple of n_kv=%d", d.n_q, d.n_kv);
+  const int g = d.n_q / d.n_kv;
+  LKV_CHECK_ARG(g == 1 || g == 2 || g == 4 || g == 8, "unsupported GQA group size %d (1, 2, 4 or 8)", g);
+  LKV_CHECK_ARG(meta_dtype == LKV_F16 || meta_dtype == LKV_BF16, "metadata dtype must be f16 or bf16");
+  LKV_CHECK_ARG(lkv_is_model_dtype(q_dtype), "bad query dtype");
+  LKV_CHECK_ARG(rank_mode == LKV_RANK_F32 || rank_mode == LKV_RANK_MODEL, "bad rank mode");
+  LKV_CHECK_ARG(cand_offset >= 0 && n_cand > 0, "bad candidate range");
+  LKV_CHECK_ARG(n_cand <= lkv_select_max_candidates(), "%d candidate blocks exceed the per-head select limit %d", n_cand,
+                lkv_select_max_candidates());
+  LKV_CHECK_ARG(d.k > 0 && d.k <= n_cand && d.attend_selected, "selected k=%d must be in 1..n_cand=%d, attended", d.k, n_cand);
+  LKV_CHECK_ARG(meta_head_stride >= (int64_t)(cand_offset + n_cand) * d.head_dim, "metadata head stride too small");
+  LKV_CHECK_ARG(out_idx == nullptr || idx_stride >= d.k, "idx_stride < k");
+  const int rc = check_hybrid(d, host, slots, block_slot, block_slot_stride, slot_block, slot_block_stride);
+  if (rc != LKV_OK) return rc;
+  const size_t dec = lkv_sparse_decode_workspace_bytes(desc);
+  const size_t hyb = lkv_hybrid_decode_workspace_bytes(desc);
+  const size_t need = lkv_select_hybrid_decode_workspace_bytes(desc, n_cand);
+  LKV_CHECK_ARG(ws != nullptr && ws_bytes >= need, "workspace of %zu bytes needed, got %zu", need, ws_bytes);
+  LKV_CHECK_ARG(((uintptr_t)ws & 15) == 0, "workspace must be 16-byte aligned");
+  int32_t* loc = (int32_t*)((char*)ws + dec);  // after the partials (dec is a multiple of 256)
+  FusedSelect fs{};
+  fs.kmin = kmin;
+  fs.kmax = kmax;
+  fs.meta_dtype = meta_dtype;
+  fs.meta_head_stride = meta_head_stride;
+  fs.rank_mode = rank_mode;
+  fs.bounds = (float*)((char*)ws + hyb);  // after the residency locations (hyb is a multiple of 256)
+  fs.stride = (int64_t)lkv_align_up((size_t)n_cand, 4);
+  fs.n_cand = n_cand;
+  fs.cand_offset = cand_offset;
+  fs.aligned = true;
+  fs.in_decode = false;
+  fs.in_residency = n_cand <= kSelCap;
+  if (out_idx != nullptr) {
+    fs.ids = out_idx;
+    fs.ids_stride = idx_stride;
+  } else {
+    fs.ids = (int32_t*)((char*)fs.bounds + lkv_align_up((size_t)d.n_kv * (size_t)fs.stride * 4, 256));
+    fs.ids_stride = d.k;
+  }
+  const ResidencyArgs res{block_slot, block_slot_stride, slot_block, slot_block_stride};
+  return sparse_decode_impl(stream, desc, q, q_dtype, host, nullptr, 0, sink, cur, nullptr, out, out_dtype, lse, ws, dec, slots, loc,
+                            (int64_t)d.k, &res, &fs);
 }

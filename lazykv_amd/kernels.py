@@ -402,6 +402,79 @@ class PreparedHybridDecode:
             _lib.check(rc, "hybrid_decode")
 
 
+class PreparedSelectHybridDecode:
+    """`lkv_select_hybrid_decode` with its arguments converted once: the Quest bound of candidates
+    cand_offset .. cand_offset + n_cand - 1 from metadata `[1, h, cap, d]`, the top k per head chosen
+    by the launch that updates `res`'s tables, and the hybrid decode over sink + selected (hits from
+    `res`'s slots, misses from `host`) + current. Equals `PreparedBoundTopk` followed by
+    `PreparedHybridDecode`, bit for bit. `desc.fill` / `desc.cur_block` and `n_cand`
+    (`set_candidates`, within `max_cand`) may change between calls."""
+
+    def __init__(self, q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, block_size: int,
+                 scale: float, host: Source, res: Residency, sink: Source | None, sink_block: int, cur: Source | None, cur_block: int, fill: int,
+                 out: torch.Tensor, lse: torch.Tensor, rank_mode: int = _lib.RANK_F32, out_idx: torch.Tensor | None = None,
+                 ws: Workspace | None = None, max_cand: int | None = None) -> None:
+        _lib.require_cuda(q, kmin, kmax, out, lse, res.slots, res.block_slot, res.slot_block)
+        n_kv, cap, d, hs = _meta_layout(kmin, kmax)
+        qq = q.reshape(-1, d)
+        if not qq.is_contiguous() or qq.shape[0] % n_kv:
+            raise ValueError("query must be contiguous [n_q, d] with n_q a multiple of the KV heads")
+        if cand_offset < 0 or n_cand <= 0 or cand_offset + n_cand > cap or not 0 < k <= n_cand:
+            raise ValueError(f"candidates {cand_offset}..{cand_offset + n_cand} of {cap} metadata blocks, k={k}")
+        if not out.is_contiguous() or out.numel() != qq.numel() or not lse.is_contiguous() or lse.numel() != qq.shape[0] or lse.dtype != torch.float32:
+            raise ValueError("out must be contiguous [n_q, d] and lse contiguous float32 [n_q]")
+        if out_idx is not None and (out_idx.dtype != torch.int32 or tuple(out_idx.shape) != (n_kv, k) or not out_idx.is_contiguous()):
+            raise ValueError(f"out_idx must be contiguous int32 [{n_kv}, {k}]")
+        for t, shape in ((res.block_slot, (n_kv, host.n_blocks)), (res.slot_block, (n_kv, k))):
+            if t.dtype != torch.int32 or t.ndim != 2 or tuple(t.shape[:1]) != shape[:1] or t.shape[1] < shape[1] or t.stride(1) != 1:
+                raise ValueError(f"residency table must be int32 [{shape[0]}, >= {shape[1]}] with contiguous rows, got {tuple(t.shape)} {t.dtype}")
+        if res.slots.shape[0] != k:
+            raise ValueError(f"the slot pool must hold k={k} slots, got {res.slots.shape[0]}")
+        self.desc = _select_desc(qq, n_kv, block_size, scale, k, sink_block, cur_block, fill)
+        ws = ws or default_workspace(q.device)
+        sizing = max(n_cand, max_cand or 0)
+        ws_ptr, ws_n = ws.get(_lib.lib().lkv_select_hybrid_decode_workspace_bytes(ctypes.byref(self.desc), sizing))
+        self._c = [s.c() if s is not None else None for s in (host, pool_source(res.slots), sink, cur)]
+        refs = [ctypes.byref(c) if c is not None else None for c in self._c]
+        self._keep = (q, kmin, kmax, out, lse, out_idx, ws.buf, host, res, sink, cur)
+        self._fn = _lib.lib().lkv_select_hybrid_decode
+        self._head = (ctypes.byref(self.desc), qq.data_ptr(), _lib.dtype_code(qq.dtype), address(kmin[0] if kmin.ndim == 4 else kmin),
+                      address(kmax[0] if kmax.ndim == 4 else kmax), _lib.dtype_code(kmin.dtype), hs, cand_offset)
+        self._tail = (rank_mode, refs[0], refs[1], res.block_slot.data_ptr(), res.block_slot.stride(0), res.slot_block.data_ptr(),
+                      res.slot_block.stride(0), refs[2], refs[3], out.data_ptr(), _lib.dtype_code(out.dtype), lse.data_ptr(),
+                      out_idx.data_ptr() if out_idx is not None else None, k, ws_ptr, ws_n)
+        self.n_cand = n_cand
+        self._cap = cap - cand_offset
+        self.device = q.device
+
+    def set_candidates(self, n_cand: int) -> None:
+        if not self.desc.k <= n_cand <= self._cap:
+            raise ValueError(f"{n_cand} candidates for k={self.desc.k}")
+        self.n_cand = n_cand
+
+    def __call__(self) -> None:
+        rc = self._fn(torch.cuda.current_stream(self.device).cuda_stream, *self._head, self.n_cand, *self._tail)
+        if rc:
+            _lib.check(rc, "select_hybrid_decode")
+
+
+def select_hybrid_decode(q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, block_size: int,
+                         scale: float, host: Source, res: Residency, sink: Source | None = None, sink_block: int = -1, cur: Source | None = None,
+                         cur_block: int = -1, fill: int = 0, rank_mode: int = _lib.RANK_F32, out: torch.Tensor | None = None,
+                         out_dtype: torch.dtype | None = None, lse: torch.Tensor | None = None, out_idx: torch.Tensor | None = None,
+                         ws: Workspace | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Bound + top-k + hybrid decode of one layer (lkv_select_hybrid_decode). Returns (out [n_q, d], lse [n_q])."""
+    qq = q.reshape(-1, q.shape[-1]).contiguous()
+    n_q, d = qq.shape
+    out_dtype = out_dtype or (out.dtype if out is not None else qq.dtype)
+    out = out if out is not None else torch.empty((n_q, d), dtype=out_dtype, device=q.device)
+    lse = lse if lse is not None else torch.empty((n_q,), dtype=torch.float32, device=q.device)
+    PreparedSelectHybridDecode(qq, kmin, kmax, k, cand_offset=cand_offset, n_cand=n_cand, block_size=block_size, scale=scale, host=host, res=res,
+                               sink=sink, sink_block=sink_block, cur=cur, cur_block=cur_block, fill=fill, out=out, lse=lse, rank_mode=rank_mode,
+                               out_idx=out_idx, ws=ws)()
+    return out, lse
+
+
 # -- a8: merge --------------------------------------------------------------------------------------
 
 

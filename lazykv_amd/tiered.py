@@ -461,10 +461,10 @@ class TieredLayer:
         return idx.to(torch.int64).cpu().numpy()
 
     def fused_select(self) -> bool:
-        """Whether a decode without given ids makes the whole step one call (lkv_select_decode):
-        zero-copy or resident reads, no exact remainder."""
+        """Whether a decode without given ids makes the whole step one call: lkv_select_decode for
+        zero-copy or resident reads, lkv_select_hybrid_decode for hybrid ones; no exact remainder."""
         n_full, _ = self.candidates()
-        return self.res is None and not self.exact and self.k <= n_full - 1
+        return not self.exact and self.k <= n_full - 1
 
     def decode(self, query: torch.Tensor, scaling: float | None, idx: torch.Tensor | None = None, out: torch.Tensor | None = None, lse: torch.Tensor | None = None, ws: kernels.Workspace | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         """Attention of one decode token over this layer's attended set. Returns out [n_q, d], lse [n_q].
@@ -479,6 +479,10 @@ class TieredLayer:
                 qq = qq.contiguous()
             out = out if out is not None else torch.empty(qq.shape, dtype=qq.dtype, device=qq.device)
             lse = lse if lse is not None else torch.empty((qq.shape[0],), dtype=torch.float32, device=qq.device)
+            if self.res is not None:
+                return kernels.select_hybrid_decode(qq, self.kmin, self.kmax, self.k, cand_offset=1, n_cand=n_full - 1, block_size=self.bs, scale=scale,
+                                                    host=self._host_src, res=self.res, sink=self._pool_src, sink_block=0, cur=self._pool_src,
+                                                    cur_block=1 if fill > 0 else -1, fill=fill, rank_mode=self.rank_mode, out=out, lse=lse, ws=ws)
             sel = self._store_src if self.fetch == "resident" else self._host_src
             return kernels.select_decode(qq, self.kmin, self.kmax, self.k, cand_offset=1, n_cand=n_full - 1, block_size=self.bs, scale=scale, sel=sel,
                                          sink=self._pool_src, sink_block=0, cur=self._pool_src, cur_block=1 if fill > 0 else -1, fill=fill,

@@ -83,6 +83,53 @@ def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, 
     assert hits > 0  # the drift keeps part of each selection resident
 
 
+@pytest.mark.parametrize(
+    ("h", "g", "n", "bs", "d", "k", "dt", "quant", "mode"),
+    [
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, None, "f32"),
+        (4, 4, 200, 16, 64, 24, torch.float16, "int8", "f32"),
+        (2, 8, 150, 32, 128, 40, torch.bfloat16, None, "model"),
+        (8, 4, 1200, 16, 64, 200, torch.float16, "int8", "model"),
+        (2, 4, 8194, 16, 64, 512, torch.bfloat16, None, "f32"),  # 8,192 candidates: the largest selected in the residency launch
+        (2, 4, 8300, 16, 64, 512, torch.bfloat16, None, "f32"),  # beyond: the selection takes its own launch
+    ],
+)
+def test_one_call_hybrid_step_is_bound_topk_then_hybrid_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, quant: str | None, mode: str) -> None:
+    """lkv_select_hybrid_decode against lkv_bound_topk + lkv_hybrid_decode from the same empty
+    tables over a drifting sequence: the same ids, tables, slot contents, output and LSE, bit for
+    bit, at every step."""
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+
+    w, pool, host, kmin, kmax = _layer(n + k + 1, h, g, n, bs, d, dt)
+    hsrc = kernels.pool_source(host)
+    if quant == "int8":
+        recs = kernels.pack_int8(pool.reshape(n * h, 2, bs, d))
+        host = pinned_empty((n, h, recs.shape[1]), torch.uint8)
+        host.copy_(recs.reshape(n, h, -1))
+        hsrc = kernels.record_source(host, dt)
+    rank = kernels._lib.RANK_F32 if mode == "f32" else kernels._lib.RANK_MODEL
+    dev = torch.device("cuda")
+    res_a = kernels.Residency.allocate(k, h, n, bs, d, dt, dev)
+    res_b = kernels.Residency.allocate(k, h, n, bs, d, dt, dev)
+    ss = kernels.pool_source(pool[[0, n - 1]].contiguous())
+    common = dict(block_size=bs, scale=d**-0.5, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=bs - 3, out_dtype=torch.float32)
+    gen = torch.Generator().manual_seed(9)
+    q0 = w.query.float()
+    idx_b = torch.empty((h, k), dtype=torch.int32, device="cuda")
+    for step in range(6):
+        q = (q0 + 0.3 * torch.randn(q0.shape, generator=gen)).to(dt).cuda()
+        idx_a = kernels.bound_topk(q, kmin, kmax, k, cand_offset=1, n_cand=n - 2, rank_mode=rank)
+        out_a, lse_a = kernels.hybrid_decode(q, n_kv=h, host=hsrc, res=res_a, idx=idx_a, **common)
+        out_b, lse_b = kernels.select_hybrid_decode(q, kmin, kmax, k, cand_offset=1, n_cand=n - 2, host=hsrc, res=res_b, rank_mode=rank, out_idx=idx_b, **common)
+        torch.cuda.synchronize()
+        assert torch.equal(idx_b, idx_a), step
+        assert torch.equal(out_b, out_a) and torch.equal(lse_b, lse_a), step
+        assert torch.equal(res_b.block_slot, res_a.block_slot) and torch.equal(res_b.slot_block, res_a.slot_block), step
+        assert torch.equal(res_b.slots, res_a.slots), step
+    assert (res_b.block_slot >= 0).any()
+
+
 @pytest.mark.parametrize("tables", ["zeros", "garbage"])
 def test_hybrid_decode_survives_tables_that_disagree(tables: str) -> None:
     """Tables filled with zeros instead of -1, or with out-of-range and contradictory entries: a
