@@ -1273,6 +1273,7 @@ struct ResSelect {
   int64_t ids_stride;
 };
 constexpr int kResSelKpt = kSelCap / kResThreads;  // candidates per thread of a selecting residency launch
+constexpr int kResCacheBlocks = 8192;               // block_slot rows up to this long are read into LDS
 
 template <bool SEL>
 __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int k,
@@ -1286,7 +1287,31 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   using SelLds = typename std::conditional<SEL, lkv::SelectLds<kResThreads, kResSelKpt>, char>::type;
   __shared__ SelLds s_sel;
   __shared__ int32_t s_ids[SEL ? kMaxSlots : 1];
+  __shared__ int32_t s_bslot[kResCacheBlocks];
+  __shared__ int32_t s_sblock[kMaxSlots];
   const int h = blockIdx.x;
+  int32_t* bslot_h = block_slot + (int64_t)h * bslot_stride;
+  int32_t* sblock_h = slot_block + (int64_t)h * sblock_stride;
+  // Rows of up to kResCacheBlocks blocks: both tables are read into LDS once, their loads issued
+  // ahead of the selection, and every lookup below is an LDS read instead of a chain of dependent
+  // global ones. The lookups see the tables as they were before this call, as the global reads
+  // did: the only entries this call writes are those of selected blocks and of blocks evicted
+  // from unhit slots, and no lookup reads an entry another thread writes. Updates go to memory.
+  const bool cached = n_blocks <= kResCacheBlocks;
+  constexpr int kTb = kResCacheBlocks / kResThreads, kTs = kMaxSlots / kResThreads;
+  int32_t tb[kTb], ts[kTs];
+  if (cached) {
+#pragma unroll
+    for (int u = 0; u < kTb; ++u) {
+      const int i = threadIdx.x + u * kResThreads;
+      tb[u] = i < n_blocks ? bslot_h[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kTs; ++u) {
+      const int i = threadIdx.x + u * kResThreads;
+      ts[u] = i < k ? sblock_h[i] : -1;
+    }
+  }
   if constexpr (SEL) {
     // The head's top k, ascending, into LDS for the residency pass and to `ids` for the decode.
     const lkv::SelectPick pk = lkv::block_top_k<kResThreads, kResSelKpt>(rs.bounds + (int64_t)h * rs.bound_stride, rs.aligned != 0, rs.n_cand, k, s_sel);
@@ -1309,9 +1334,20 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   const int per = (k + kResThreads - 1) / kResThreads;  // <= kResPer
   const int i0 = threadIdx.x * per;
   const int32_t* idx_h = idx + (int64_t)h * idx_stride;
-  int32_t* bslot_h = block_slot + (int64_t)h * bslot_stride;
-  int32_t* sblock_h = slot_block + (int64_t)h * sblock_stride;
   for (int i = threadIdx.x; i < kMaxSlots / 32; i += kResThreads) hit[i] = 0u;
+  if (cached) {
+#pragma unroll
+    for (int u = 0; u < kTb; ++u) {
+      const int i = threadIdx.x + u * kResThreads;
+      if (i < n_blocks) s_bslot[i] = tb[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kTs; ++u) {
+      const int i = threadIdx.x + u * kResThreads;
+      if (i < k) s_sblock[i] = ts[u];
+    }
+    __syncthreads();
+  }
   // This thread's items [i0, i0 + per): their blocks and current slots.
   int32_t blk[kResPer], cur[kResPer];
 #pragma unroll
@@ -1319,7 +1355,7 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
     const int i = i0 + u;
     blk[u] = (u < per && i < k) ? (SEL ? s_ids[i] : idx_h[i]) : -1;
     const bool valid = blk[u] >= 0 && (int64_t)blk[u] < n_blocks;
-    cur[u] = valid ? bslot_h[blk[u]] : -2;  // -2: not a block of the pool; -1: not resident
+    cur[u] = valid ? (cached ? s_bslot[blk[u]] : bslot_h[blk[u]]) : -2;  // -2: not a block of the pool; -1: not resident
     if (valid && (cur[u] < 0 || cur[u] >= n_slots)) cur[u] = -1;  // an entry that names no slot: not resident
   }
   // A hit needs both tables to agree (block_slot[b] = s and slot_block[s] = b): tables a caller
@@ -1327,7 +1363,7 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   // a slot that holds another block.
 #pragma unroll
   for (int u = 0; u < kResPer; ++u)
-    if (cur[u] >= 0 && sblock_h[cur[u]] != blk[u]) cur[u] = -1;
+    if (cur[u] >= 0 && (cached ? s_sblock[cur[u]] : sblock_h[cur[u]]) != blk[u]) cur[u] = -1;
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < kResPer; ++u)
@@ -1364,10 +1400,10 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
       loc_h[i] = -1;  // outside the pool (or no slot left, which a consistent table rules out)
     } else {
       const int v = victims[mpos++];
-      const int32_t old = sblock_h[v];
+      const int32_t old = cached ? s_sblock[v] : sblock_h[v];
       // Only an entry that points back at v is cleared: then `old` was resident in v, and as v is
       // unhit, `old` is unselected, so no other item writes its entry.
-      if (old >= 0 && (int64_t)old < n_blocks && bslot_h[old] == v) bslot_h[old] = -1;
+      if (old >= 0 && (int64_t)old < n_blocks && (cached ? s_bslot[old] : bslot_h[old]) == v) bslot_h[old] = -1;
       sblock_h[v] = blk[u];
       bslot_h[blk[u]] = v;
       loc_h[i] = kLocMiss | v;
