@@ -387,7 +387,7 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
                               fill=fill, out=outs[li], lse=lses[li], ws=ws_dec)
                 decodes.append(kernels.PreparedSelectDecode(st["q"], st["kmin"], st["kmax"], k, **common))
                 checks.append(kernels.PreparedSelectDecode(st["q"], st["kmin"], st["kmax"], k, out_idx=idx, **common))
-                if n_cand > kernels._lib.SELECT_IN_DECODE_MAX_CAND:
+                if not kernels._lib.selects_in_decode(n_cand, bool(sels[li].flags), N_Q // H):
                     ranks.append(kernels.PreparedBoundTopk(st["q"], st["kmin"], st["kmax"], k, cand_offset=1, n_cand=n_cand, out_idx=idx, ws=ws_sel))
                 else:
                     bnd = torch.empty((H, n_cand), dtype=torch.float32, device=dev)
@@ -522,9 +522,9 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             "rank_note": "the reference's tier ranks on the bound rounded to the model dtype (top_blocks dtype=None); this step ranks on the float32 bound, "
                          "so its selected sets equal the reference's except in near-tie cells (|b_K - b_K+1| <= 1e-5 max(1, |b_K|))",
             "dense_layers": 0, "launch": "eager" if args.eager else "hip_graph",
-            "launches_per_layer": 3 if (m["fused"] and n_cand <= kernels._lib.SELECT_IN_DECODE_MAX_CAND) else 4,
+            "launches_per_layer": 3 if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H)) else 4,
             "step_kernels": ("one lkv_select_decode call: bound_kernel, sparse_decode_kernel choosing the top K itself, decode_merge_kernel"
-                             if (m["fused"] and n_cand <= kernels._lib.SELECT_IN_DECODE_MAX_CAND) else
+                             if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H)) else
                              ("one lkv_select_decode call: " if m["fused"] else "lkv_bound_topk + lkv_sparse_decode: ")
                              + "bound_kernel, select_kernel, sparse_decode_kernel, decode_merge_kernel"),
             "host_memory": "fine-grained" if args.coherent else "coarse-grained",
@@ -536,7 +536,7 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
     traffic = pmc_traffic() if kind == "host" else {}
     if m["sparse_decode_pcie_bytes"]:
         gbps = m["sparse_decode_pcie_gbps"]
-        kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and n_cand <= kernels._lib.SELECT_IN_DECODE_MAX_CAND)
+        kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H))
                  else "sparse_decode_kernel + decode_merge_kernel")
         out["roofline"] = {"bound": "pcie", "kernel": f"{kname}, host reads over PCIe", "achieved": gbps,
                            "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get("zerocopy/sparse_decode_kernel"),
@@ -550,7 +550,7 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             out["roofline"]["traffic_run"] = pmc_run("zerocopy")
     else:
         gbps = m["sparse_decode_hbm_gbps"]
-        kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and n_cand <= kernels._lib.SELECT_IN_DECODE_MAX_CAND)
+        kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H))
                  else "sparse_decode_kernel + decode_merge_kernel")
         out["roofline"] = {"bound": "hbm", "kernel": f"{kname}, HBM", "achieved": gbps,
                            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get("hbm/sparse_decode_kernel"),

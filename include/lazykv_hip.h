@@ -141,8 +141,10 @@ int lkv_sparse_decode(uintptr_t stream, const lkv_decode_desc* desc, const void*
  * the top_blocks rule of lazykv/selection.py:56-62). The bound kernel scores candidates
  * cand_offset .. cand_offset+n_cand-1 of every KV head into the workspace; each head's top desc->k
  * -- the same set as lkv_bound_topk, ties to the lower id -- is then chosen inside the decode
- * launch (up to 8,192 candidates per head: two launches for bound, top-K and attention, plus the
- * merge) or by its own launch (beyond), and the sink, the selected blocks (from `sel`) and the
+ * launch (two launches for bound, top-K and attention, plus the merge) while that launch's
+ * threads hold at most 16 candidates each -- up to 8,192 candidates per head when `sel` is in
+ * HBM, 4,096 when it is host memory -- or by its own launch beyond, and the sink, the selected
+ * blocks (from `sel`) and the
  * current block are attended as lkv_sparse_decode does. The result equals lkv_bound_topk followed
  * by lkv_sparse_decode, bit for bit. out_idx, if not NULL, receives the selected ids in ascending
  * order (idx_stride apart per head). No remainder; up to 262,144 candidates per head. */

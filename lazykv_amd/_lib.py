@@ -22,6 +22,16 @@ RANK_F32, RANK_MODEL = 0, 1
 HOST_COHERENT = 1
 SRC_HOST = 1
 SELECT_IN_DECODE_MAX_CAND = 8192  # lkv_select_decode chooses the top K inside the decode launch up to this many candidates
+
+
+def selects_in_decode(n_cand: int, host: bool, group: int) -> bool:
+    """Whether lkv_select_decode chooses the top K inside its decode launch, as the library decides:
+    up to 16 candidates per thread of that launch -- 512 threads when the selected pairs are in HBM
+    and the query group is at most 4, else 256 -- and never beyond SELECT_IN_DECODE_MAX_CAND."""
+    threads = 512 if (not host and group <= 4) else 256
+    return n_cand <= min(SELECT_IN_DECODE_MAX_CAND, 16 * threads)
+
+
 STATIC_SCRATCH_BYTES = 16 * 1024 * 1024  # LKV_STATIC_SCRATCH_BYTES: the allocation-free decode's partials per device
 
 _DTYPE_CODES = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}

@@ -762,6 +762,7 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
 // with 4,096). Longer contexts select in their own launch.
 constexpr int kSelUnit = 4096;
 constexpr int kSelCap = 2 * kSelUnit;
+constexpr int kFuseKeysPerThread = 16;  // a decode launch selects inside itself up to this many keys per thread
 template <int NT, int SEL>
 constexpr int kSelKpt = SEL * kSelUnit / NT;
 
@@ -1596,7 +1597,9 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
   a.loc = loc;
   a.loc_stride = loc_stride;
   if (slots) a.slots = to_src(slots);
-  const bool select_in_decode = fsel != nullptr && fsel->in_decode;
+  // Inside the decode launch only while each thread holds at most kFuseKeysPerThread of the head's
+  // candidates; beyond, the selection takes a launch of its own.
+  const bool select_in_decode = fsel != nullptr && fsel->in_decode && fsel->n_cand <= kFuseKeysPerThread * p.nt;
   if (fsel != nullptr) {
     LKV_CHECK_ARG(attend_sel && !has_rem, "a fused selection attends a selection, with no remainder");
     LKV_CHECK_ARG(res == nullptr || !fsel->in_decode, "a hybrid call selects before its residency launch");
@@ -1759,12 +1762,16 @@ extern "C" int lkv_sparse_decode_static(uintptr_t stream, const lkv_decode_desc*
 
 // ---- a1 + a2 + a5 + a6: one selecting layer's decode step ---------------------------------------
 // Where the top k is chosen. Inside the decode launch it saves the selection's own launch, but every
-// decode workgroup then waits for its own pass over all of the head's bounds. Measured on MI355X,
-// the in-launch selection wins at 2,046 and 4,094 candidates per head (1.5 and 1.9 us per layer at
-// the 32K- and 64K-token 1B shapes) and at 8,190 (1.6 us at the 128K-token 8B shape, with 8,192
-// key slots per workgroup). Up to kFuseMaxCand candidates it selects in the decode launch, beyond
-// it in its own (the streaming selection); the results are the same bits either way.
+// decode workgroup then waits for its own pass over all of the head's bounds, and that pass grows
+// with the keys each thread holds. Measured on MI355X (A/B, one box), the in-launch selection wins
+// with up to 16 keys per thread: at 2,046 and 4,094 candidates per head in the 512-thread HBM
+// launches (1.5 and 1.9 us per layer at the 32K- and 64K-token 1B shapes), at 8,190 there (1.6 us
+// at the 128K-token 8B shape), and at 4,094 in the 256-thread host launch (int8_64k from host
+// memory, 372.9 -> 368.9 us). At 32 keys per thread -- 8,190 candidates in a host launch, the
+// 128K-token zero-copy step -- it loses (615.1 against 620.1 us per layer), and the selection takes
+// its own launch. The results are the same bits either way.
 constexpr int kFuseMaxCand = kSelCap;
+
 
 extern "C" size_t lkv_select_decode_workspace_bytes(const lkv_decode_desc* desc, int n_cand) {
   const size_t base = lkv_sparse_decode_workspace_bytes(desc);
