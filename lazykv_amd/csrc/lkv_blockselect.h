@@ -53,9 +53,13 @@ struct SelectPick {
 
 // Exclusive prefix sum over the workgroup's threads in thread order; `slots` holds one word per
 // wave and is read after the barrier inside. The caller separates reuses of `slots` by a barrier.
-template <int NT>
+// SCALAR_WAVE reads the wave index into a scalar register, so that `w < wave` is a scalar compare
+// instead of a lane mask per w that the compiler may keep live across the passes (a launch with
+// little else to hold gains; inside the decode launch it measured slower).
+template <int NT, bool SCALAR_WAVE = false>
 __device__ __forceinline__ uint32_t workgroup_exclusive_sum(uint32_t v, uint32_t* slots, uint32_t* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = SCALAR_WAVE ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : (int)(threadIdx.x >> 6);
   const uint32_t x = wave_inclusive_sum(v);
   if (lane == 63) slots[wave] = x;
   __syncthreads();
@@ -100,7 +104,7 @@ __device__ __forceinline__ void clear_bins(uint32_t* p) {
 
 // Select k of the n bounds at `bound_h` (n <= NT * KPT; the row is readable in whole 16-byte
 // vectors up to a multiple of 4 when `aligned`). Every thread of the workgroup must call it.
-template <int NT, int KPT>
+template <int NT, int KPT, bool SCALAR_WAVE = false>
 __device__ __forceinline__ SelectPick block_top_k(const float* __restrict__ bound_h, bool aligned, int n, int k, SelectLds<NT, KPT>& L) {
   static_assert(KPT % 4 == 0 && KPT <= 32, "a thread's slots are tracked in 32-bit masks, loaded 4 at a time");
   constexpr int kWaves = NT / 64;
@@ -177,7 +181,7 @@ __device__ __forceinline__ SelectPick block_top_k(const float* __restrict__ boun
 #pragma unroll
     for (int b = 0; b < kBpt; ++b) local += cnt[b];
     uint32_t total;
-    const uint32_t below = workgroup_exclusive_sum<NT>(local, L.scan[0], &total);
+    const uint32_t below = workgroup_exclusive_sum<NT, SCALAR_WAVE>(local, L.scan[0], &total);
     const uint32_t above = total - below - local;  // keys of higher bins (owned by later threads)
     if (above < (uint32_t)need && (uint32_t)need <= above + local) {
       uint32_t acc = above;
@@ -250,7 +254,7 @@ __device__ __forceinline__ SelectPick block_top_k(const float* __restrict__ boun
   if (!tie_mode) need = 0;
   const uint32_t gt = __popc(above_m), eq = __popc(tie_m);
   uint32_t tot;
-  const uint32_t packed = workgroup_exclusive_sum<NT>((eq << 16) | gt, L.scan[1], &tot);
+  const uint32_t packed = workgroup_exclusive_sum<NT, SCALAR_WAVE>((eq << 16) | gt, L.scan[1], &tot);
   const int eq_before = (int)(packed >> 16), gt_before = (int)(packed & 0xffffu);
   int take_eq = need - eq_before;
   take_eq = take_eq < 0 ? 0 : (take_eq > (int)eq ? (int)eq : take_eq);

@@ -23,6 +23,7 @@
 // with ties broken towards the lower id. Scoring and selection are separate launches so that no
 // workgroup has to publish its bounds across XCDs inside one launch (a device-scope release
 // writes back the L2); the kernel boundary does that once.
+#include "lkv_blockselect.h"
 #include "lkv_common.h"
 
 namespace {
@@ -535,6 +536,39 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
   }
 }
 
+// ---- the unsorted selection as one in-workgroup top-K ----------------------------------------------
+// The same rule and ids as select_kernel's unsorted mode, by the routine the decode and residency
+// launches run inside themselves (lkv_blockselect.h: 2,048 bins a pass read as vectors, a direct
+// rank of a small boundary bin, an exit when that bin is taken whole), with the shape of the
+// decode launch's selection at 8,192 candidates: 512 threads of 16 keys, the wave index scalar in
+// the scans (as lane masks, the scans' wave tests spilled scalar registers), over rows that are 16-byte aligned and
+// padded to 4 floats (the workspace's). Each thread writes its ids straight to their ascending
+// output positions.
+constexpr int kSelBlockThreads = 512;
+constexpr int kSelBlockKpt = 16;
+constexpr int kSelBlockCap = kSelBlockThreads * kSelBlockKpt;  // 8,192 candidates per head
+__global__ __launch_bounds__(kSelBlockThreads) void select_block_kernel(const float* __restrict__ bounds, int64_t bstride,
+                                                                        int n_cand, int k, int cand_offset,
+                                                                        int32_t* __restrict__ out_idx, int64_t idx_stride) {
+  __shared__ lkv::SelectLds<kSelBlockThreads, kSelBlockKpt> L;
+  const int h = blockIdx.x;
+  const lkv::SelectPick pk = lkv::block_top_k<kSelBlockThreads, kSelBlockKpt, true>(bounds + (int64_t)h * bstride, true, n_cand, k, L);
+  int32_t* out_h = out_idx + (int64_t)h * idx_stride;
+  int pos = pk.pos;
+#pragma unroll
+  for (int u = 0; u < kSelBlockKpt; ++u) {
+    if ((pk.take >> u) & 1u) {
+      if (pos < k) out_h[pos] = pk.i0 + u + cand_offset;
+      ++pos;
+    }
+  }
+}
+
+// Rows the in-workgroup top-K may read as 16-byte vectors: aligned, and padded to 4 floats.
+static bool rows_vector_readable(const float* bounds, int64_t bstride, int n_cand) {
+  return ((uintptr_t)bounds & 15u) == 0 && bstride % 4 == 0 && bstride >= (int64_t)lkv_align_up((size_t)n_cand, 4);
+}
+
 // ---- select for long contexts: keys streamed from memory on every pass --------------------------
 // The same selection as select_kernel -- range-adaptive radix select of the K-th largest key, direct
 // ranking of the boundary bin, ties to the lower id, ascending or sorted output -- for heads with
@@ -792,7 +826,10 @@ int lkv_select_max_candidates() { return kMaxStreamCand; }
 
 int lkv_launch_select(hipStream_t s, const float* bounds, int64_t bstride, int n_kv, int n_cand, int k, int cand_offset,
                       int32_t* out_idx, int64_t idx_stride) {
-  if (n_cand <= kMaxCand) {
+  if (n_cand <= kSelBlockCap && rows_vector_readable(bounds, bstride, n_cand)) {
+    hipLaunchKernelGGL(select_block_kernel, dim3(n_kv), dim3(kSelBlockThreads), 0, s, bounds, bstride, n_cand, k, cand_offset,
+                       out_idx, idx_stride);
+  } else if (n_cand <= kMaxCand) {
     hipLaunchKernelGGL(select_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k, cand_offset, 0, out_idx,
                        idx_stride);
   } else {
@@ -843,7 +880,10 @@ extern "C" int lkv_bound_topk(uintptr_t stream, const void* q, int q_dtype, cons
   const int rc = lkv_launch_bounds(s, q, q_dtype, kmin, kmax, meta_dtype, meta_head_stride, n_kv, g, head_dim, cand_offset, n_cand,
                                    rank_mode, bounds, bstride);
   if (rc != LKV_OK || k == 0) return rc;
-  if (n_cand <= kMaxCand) {
+  if (n_cand <= kSelBlockCap && !sorted && rows_vector_readable(bounds, bstride, n_cand)) {
+    hipLaunchKernelGGL(select_block_kernel, dim3(n_kv), dim3(kSelBlockThreads), 0, s, bounds, bstride, n_cand, k, cand_offset,
+                       out_idx, idx_stride);
+  } else if (n_cand <= kMaxCand) {
     hipLaunchKernelGGL(select_kernel, dim3(n_kv), dim3(kSelThreads), 0, s, bounds, bstride, n_cand, k, cand_offset,
                        sorted, out_idx, idx_stride);
   } else {
