@@ -756,12 +756,12 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
 }
 
 // Candidates a fused-selection workgroup holds (KPT keys per thread): SEL * kSelUnit per KV head.
-// SEL 1 holds 4,096 (a 65,536-token context at 16-token blocks), SEL 2 holds 8,192; a launch
-// takes the smaller that fits, since every key slot a thread holds costs its instructions in each
-// selection phase (measured: the 32K-token 1B step 1.7 us slower per layer with 8,192 slots than
-// with 4,096). Longer contexts select in their own launch.
-constexpr int kSelUnit = 4096;
-constexpr int kSelCap = 2 * kSelUnit;
+// SEL 1 holds 2,048 (a 32,768-token context at 16-token blocks), SEL 2 holds 4,096, SEL 4 holds
+// 8,192; a launch takes the smallest that fits, since every key slot a thread holds costs its
+// instructions in each selection phase (measured: the 32K-token 1B step 1.7 us slower per layer
+// with 8,192 slots than with 4,096). Longer contexts select in their own launch.
+constexpr int kSelUnit = 2048;
+constexpr int kSelCap = 4 * kSelUnit;
 constexpr int kFuseKeysPerThread = 16;  // a decode launch selects inside itself up to this many keys per thread
 template <int NT, int SEL>
 constexpr int kSelKpt = SEL * kSelUnit / NT;
@@ -1214,9 +1214,10 @@ int launch(hipStream_t stream, DecodeArgs& a) {
   if ((inst == Inst::kMatrix8 && (MT == LKV_F32 || G > 4)) || (inst == Inst::kInt8x8 && (G > 4 || (D == 128 && G == 4))) ||
       (inst == Inst::kVector8 && (G > 4 || sel)))
     inst = Inst::kGeneral;  // no such instance (pick_instance never asks for one)
-  const int rc = !sel                      ? launch_inst<D, MT, G, 0>(stream, a, inst)
-                 : a.n_cand <= kSelUnit ? launch_inst<D, MT, G, 1>(stream, a, inst)
-                                        : launch_inst<D, MT, G, 2>(stream, a, inst);
+  const int rc = !sel                          ? launch_inst<D, MT, G, 0>(stream, a, inst)
+                 : a.n_cand <= kSelUnit     ? launch_inst<D, MT, G, 1>(stream, a, inst)
+                 : a.n_cand <= 2 * kSelUnit ? launch_inst<D, MT, G, 2>(stream, a, inst)
+                                            : launch_inst<D, MT, G, 4>(stream, a, inst);
   if (rc != LKV_OK) return rc;
   hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(512), 0, stream, a.part_ml, a.part_o, S,
                      a.out, a.out_dtype, a.lse);
