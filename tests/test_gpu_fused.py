@@ -49,6 +49,10 @@ CASES = [
     (4, 2, 130, 32, 64, 100, 1, torch.float16, "host"),
     (1, 4, 700, 16, 64, 3, 16, torch.bfloat16, "hbm"),
     (4, 1, 60, 64, 128, 58, 60, torch.float16, "hbm"),  # every candidate selected
+    (2, 4, 2050, 16, 64, 300, 3, torch.float16, "hbm"),  # 2,048 candidates: the most in 2,048 key slots
+    (2, 4, 2051, 16, 64, 300, 3, torch.float16, "hbm"),  # 2,049: 4,096 key slots
+    (2, 4, 4098, 16, 128, 300, 3, torch.bfloat16, "host"),  # 4,096: the most a host launch selects inside itself
+    (2, 4, 4099, 16, 128, 300, 3, torch.bfloat16, "host"),  # 4,097 from host memory: the top-K in its own launch
     (2, 4, 4098, 16, 64, 300, 3, torch.bfloat16, "hbm"),  # 4,096 candidates: the most in 4,096 key slots
     (2, 4, 4099, 16, 64, 300, 3, torch.bfloat16, "hbm"),  # 4,097: 8,192 key slots
     (2, 4, 8194, 16, 64, 600, 3, torch.float16, "hbm"),  # 8,192: the most selected inside the decode launch
