@@ -184,6 +184,17 @@ def test_hybrid_decode_refuses_what_it_cannot_hold() -> None:
     wrong = kernels.Residency.allocate(k + 1, h, n, bs, d, torch.float16, torch.device("cuda"))
     with pytest.raises(ValueError, match="slots"):
         kernels.hybrid_decode(w.query.cuda(), n_kv=h, block_size=bs, scale=d**-0.5, host=kernels.pool_source(host), res=wrong, idx=idx)
+    common = dict(cand_offset=1, block_size=bs, scale=d**-0.5, host=kernels.pool_source(host))
+    with pytest.raises(ValueError, match="slots"):
+        kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, k, n_cand=n - 2, res=wrong, **common)
+    right = kernels.Residency.allocate(k, h, n, bs, d, torch.float16, torch.device("cuda"))
+    with pytest.raises(ValueError, match="candidates"):
+        kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, k, n_cand=n, res=right, **common)  # past the metadata
+    with pytest.raises(ValueError, match="k="):
+        kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, n, n_cand=n - 2, res=right, **common)  # more than the candidates
+    short = kernels.Residency(right.slots, right.block_slot[:, : n - 5].contiguous(), right.slot_block)
+    with pytest.raises(ValueError, match="residency table"):
+        kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, k, n_cand=n - 2, res=short, **common)
 
 
 def test_hybrid_cache_decodes_like_the_zero_copy_cache() -> None:
