@@ -539,13 +539,14 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(const float* __rest
 // ---- the unsorted selection as one in-workgroup top-K ----------------------------------------------
 // The same rule and ids as select_kernel's unsorted mode, by the routine the decode and residency
 // launches run inside themselves (lkv_blockselect.h: 2,048 bins a pass read as vectors, a direct
-// rank of a small boundary bin, an exit when that bin is taken whole), with the shape of the
-// decode launch's selection at 8,192 candidates: 512 threads of 16 keys, the wave index scalar in
-// the scans (as lane masks, the scans' wave tests spilled scalar registers), over rows that are 16-byte aligned and
-// padded to 4 floats (the workspace's). Each thread writes its ids straight to their ascending
-// output positions.
-constexpr int kSelBlockThreads = 512;
-constexpr int kSelBlockKpt = 16;
+// rank of a small boundary bin, an exit when that bin is taken whole), with 1,024 threads of 8 keys
+// (8,192 candidates per head; every key slot a thread holds costs instructions in each phase, and
+// against 512 threads of 16 the 128K-token zero-copy step measured 615.23 -> 614.47 us per layer),
+// the wave index scalar in the scans (as lane masks, the scans' wave tests spilled scalar
+// registers), over rows that are 16-byte aligned and padded to 4 floats (the workspace's). Each
+// thread writes its ids straight to their ascending output positions.
+constexpr int kSelBlockThreads = 1024;
+constexpr int kSelBlockKpt = 8;
 constexpr int kSelBlockCap = kSelBlockThreads * kSelBlockKpt;  // 8,192 candidates per head
 __global__ __launch_bounds__(kSelBlockThreads) void select_block_kernel(const float* __restrict__ bounds, int64_t bstride,
                                                                         int n_cand, int k, int cand_offset,
