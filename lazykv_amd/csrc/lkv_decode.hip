@@ -1244,7 +1244,7 @@ int dispatch_g(int g, hipStream_t s, DecodeArgs& a) {
 // block_slot[h][b] = slot or -1, slot_block[h][s] = block or -1. Writes loc[h][j] for the decode:
 // the slot of a hit, kLocMiss | slot for a miss (read from the host, copied into the slot), or -1
 // for an id outside the pool (attended nowhere, like the plain path).
-constexpr int kResThreads = 512;
+constexpr int kResThreads = 1024;  // 1,024 threads: a selecting launch holds 8 keys per thread (16 at 512 were slower)
 constexpr int kMaxSlots = 4096;
 constexpr int kResPer = kMaxSlots / kResThreads;  // items and slots per thread
 
@@ -1316,7 +1316,7 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   }
   if constexpr (SEL) {
     // The head's top k, ascending, into LDS for the residency pass and to `ids` for the decode.
-    const lkv::SelectPick pk = lkv::block_top_k<kResThreads, kResSelKpt>(rs.bounds + (int64_t)h * rs.bound_stride, rs.aligned != 0, rs.n_cand, k, s_sel);
+    const lkv::SelectPick pk = lkv::block_top_k<kResThreads, kResSelKpt, true>(rs.bounds + (int64_t)h * rs.bound_stride, rs.aligned != 0, rs.n_cand, k, s_sel);
     int32_t* ids_h = rs.ids + (int64_t)h * rs.ids_stride;
     int pos = pk.pos;
 #pragma unroll
