@@ -294,8 +294,15 @@ struct Widen {
   }
 };
 
-// Dequantisation (quant.py:103-105): ((q + 128) * scale) + zero, float32 multiply and add rounded
-// separately (this file is built without FP contraction), then rounded to the model dtype.
+// Dequantisation (quant.py:103-105): ((q + 128) * scale) + zero in float32, then rounded to the
+// model dtype. q + 128 is the code byte with its top bit flipped, read unsigned (one byte
+// conversion, no add). The product of that 8-bit integer and a float16 scale has at most 19
+// significant bits, so float32 holds it exactly: the reference's separately rounded multiply and
+// add equal one fused multiply-add, which rounds once (checked on the CPU for every float16 scale,
+// every code and 512 zeros, specials included). The float32 result is pinned in a register before
+// its conversion: left free, the compiler fuses the FMA and the conversion into one mixed-precision
+// FMA with a float16 result (v_fma_mixlo_f16), which rounds once, straight to float16 -- 8.0078
+// where the reference's float32 rounding lands on a tie and gives 8.
 template <int D, int MT>
 struct WidenI8 {
   using Raw = RawI8<D>;
@@ -308,18 +315,23 @@ struct WidenI8 {
       kz[e] = lkv::f16_to_f32((uint16_t)((e & 1) ? (raw.kz[e >> 1] >> 16) : (raw.kz[e >> 1] & 0xffffu)));
     }
   }
-  __device__ __forceinline__ static float q8(const uint32_t* w, int e) {
-    return (float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xffu);
+  __device__ __forceinline__ static float u8(const uint32_t* w, int e) {  // q + 128 of element e
+    return (float)(((w[e >> 2] ^ 0x80808080u) >> (8 * (e & 3))) & 0xffu);
+  }
+  __device__ __forceinline__ static float deq(float u, float s, float z) {  // rounded to float32
+    float x = fmaf(u, s, z);
+    asm("" : "+v"(x));
+    return x;
   }
   __device__ __forceinline__ void key(const Raw& raw, int i, float (&x)[EPL]) const {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) x[e] = lkv::round_through<MT>((q8(raw.k[i], e) + 128.0f) * ks[e] + kz[e]);
+    for (int e = 0; e < EPL; ++e) x[e] = lkv::round_through<MT>(deq(u8(raw.k[i], e), ks[e], kz[e]));
   }
   __device__ __forceinline__ void value(const Raw& raw, int i, float (&x)[EPL]) const {
     const float vs = lkv::f16_to_f32((uint16_t)raw.vs[i]);
     const float vz = lkv::f16_to_f32((uint16_t)raw.vz[i]);
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) x[e] = lkv::round_through<MT>((q8(raw.v[i], e) + 128.0f) * vs + vz);
+    for (int e = 0; e < EPL; ++e) x[e] = lkv::round_through<MT>(deq(u8(raw.v[i], e), vs, vz));
   }
 };
 

@@ -83,6 +83,51 @@ def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, 
     assert hits > 0  # the drift keeps part of each selection resident
 
 
+@pytest.mark.parametrize(("dt", "d", "u", "scale_bits"), [(torch.float16, 64, 145, 0x01C4), (torch.bfloat16, 128, 185, 0x0989)])
+def test_int8_miss_fill_rounds_like_the_reference(dt: torch.dtype, d: int, u: int, scale_bits: int) -> None:
+    """Records planted so that one key channel and one value token dequantise to u * s + 8 just
+    above a tie of the model dtype: quant.py:103-105 rounds to float32 first, which lands on the
+    tie and rounds to 8. The decode's in-register dequantisation (here: the hybrid miss fill, whose
+    slot rows are those values) and lkv_unpack_int8 must both give the oracle's rows bit for bit,
+    8 at every planted element; the hybrid output equals the zero-copy output."""
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+
+    h, g, n, bs, k, c0, t0 = 2, 4, 40, 16, 8, 5, 3
+    name = "f16" if dt == torch.float16 else "bf16"
+    w, pool, _, _, _ = _layer(11, h, g, n, bs, d, dt)
+    recs = kernels.pack_int8(pool.reshape(n * h, 2, bs, d)).cpu().numpy()
+    o1, o2, o3, o4, o5 = R.record_offsets(bs, d)
+    code = u ^ 0x80  # the int8 code u - 128, as a byte
+    recs[:, [t * d + c0 for t in range(bs)]] = code  # key channel c0 of every token
+    recs[:, o1 + t0 * d : o1 + (t0 + 1) * d] = code  # every channel of value token t0
+    for at, val in ((o2 + 2 * c0, scale_bits), (o3 + 2 * c0, 0x4800), (o4 + 2 * t0, scale_bits), (o5 + 2 * t0, 0x4800)):
+        recs[:, at : at + 2] = np.array([val], dtype="<u2").view(np.uint8)  # float16, little-endian; 0x4800 = 8.0
+    recs_np = np.ascontiguousarray(recs)
+    want = torch.from_numpy(R.unpack(recs_np, bs, d, name).view(np.int16)).view(dt).reshape(n, h, 2, bs, d)
+    assert torch.all(want[:, :, 0, :, c0] == 8.0) and torch.all(want[:, :, 1, t0, :] == 8.0)
+    recs_gpu = torch.from_numpy(recs_np).cuda()
+    assert torch.equal(kernels.unpack_int8(recs_gpu, bs, d, dt).cpu().view(torch.int16), want.reshape(n * h, 2, bs, d).view(torch.int16))
+    host = pinned_empty((n, h, recs_np.shape[1]), torch.uint8)
+    host.copy_(torch.from_numpy(recs_np).reshape(n, h, -1))
+    hsrc = kernels.record_source(host, dt)
+    res = kernels.Residency.allocate(k, h, n, bs, d, dt, torch.device("cuda"))
+    ss = kernels.pool_source(pool[[0, n - 1]].contiguous())
+    idx = torch.arange(2, 2 + 3 * k, 3, dtype=torch.int32).repeat(h, 1).cuda()
+    q = w.query.cuda()
+    common = dict(n_kv=h, block_size=bs, scale=d**-0.5, idx=idx, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=9, out_dtype=torch.float32)
+    out_z, lse_z = kernels.sparse_decode(q, sel=hsrc, **common)
+    out_h, lse_h = kernels.hybrid_decode(q, host=hsrc, res=res, **common)
+    torch.cuda.synchronize()
+    assert torch.equal(out_h, out_z) and torch.equal(lse_h, lse_z)
+    sb = res.slot_block.cpu()
+    assert sorted(sb[0].tolist()) == idx[0].cpu().tolist()
+    for j in range(h):
+        got = res.slots[:, j].cpu()
+        assert torch.equal(got.view(torch.int16), want[sb[j].long(), j].view(torch.int16)), j
+        assert torch.all(got[:, 0, :, c0] == 8.0) and torch.all(got[:, 1, t0, :] == 8.0), j
+
+
 @pytest.mark.parametrize(
     ("h", "g", "n", "bs", "d", "k", "dt", "quant", "mode"),
     [

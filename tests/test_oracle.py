@@ -107,6 +107,32 @@ def test_quantiser_rounds_half_to_even() -> None:
     assert kq[2] == 2 and kq[3] == 4  # 2.5 -> 2, 3.5 -> 4
 
 
+@pytest.mark.parametrize(("dt", "u", "scale_bits", "single"), [("f16", 145, 0x01C4, 8.0078125), ("bf16", 185, 0x0989, 8.0625)])
+def test_unpack_rounds_to_float32_before_the_model_dtype(dt: str, u: int, scale_bits: int, single: float) -> None:
+    """quant.py:103-105 dequantises in float32 and then casts. With code u (q = u - 128), the
+    scale s given and zero 8, the exact u * s + 8 lies just above a tie of the model dtype between
+    8 and `single`; float32 rounding lands on the tie, which then rounds to the even 8. A
+    dequantisation that rounds once (float64, or one fused rounding into the model dtype) gives
+    `single` instead."""
+    from fractions import Fraction
+
+    bs, d = 4, 8
+    s = np.array([scale_bits], dtype=np.uint16).view(np.float16)[0]
+    exact = Fraction(u) * Fraction(float(s)) + 8
+    tie = (Fraction(8) + Fraction(single)) / 2
+    assert tie < exact < tie + Fraction(1, 2**20)  # above the tie by less than half a float32 ulp at 8
+    o1, o2, o3, o4, o5 = R.record_offsets(bs, d)
+    rec = np.zeros((1, R.packed_pair_bytes(bs, d)), dtype=np.uint8)
+    rec[0, :o2] = u ^ 0x80  # the int8 code u - 128
+    rec[0, o2:o3] = np.full(d, scale_bits, dtype=np.uint16).view(np.uint8)
+    rec[0, o3:o4] = np.full(d, 0x4800, dtype=np.uint16).view(np.uint8)  # float16 8.0
+    rec[0, o4:o5] = np.full(bs, scale_bits, dtype=np.uint16).view(np.uint8)
+    rec[0, o5:] = np.full(bs, 0x4800, dtype=np.uint16).view(np.uint8)
+    assert np.all(R.unpack_f32(rec, bs, d) == np.float32(float(tie)))
+    assert np.all(R.to_f32(R.unpack(rec, bs, d, dt), dt) == 8.0)
+    assert np.all(quant_c.unpack(rec, bs, d, dt) == R.unpack(rec, bs, d, dt))
+
+
 def test_rejects_bad_widths_and_pairs() -> None:
     """tests/test_quant.py:66-73."""
     with pytest.raises(ValueError, match="packed_pair_bytes"):
