@@ -232,6 +232,18 @@ def _pmc_file() -> dict:
         return {}
 
 
+def step_kernels(fused: bool, in_decode: bool, n_cand: int) -> str:
+    """One layer's launches, as rocprof names them, by the library's dispatch rules: the matrix-core
+    bound for a model-dtype query with aligned rows; the top K inside the decode launch when the
+    fused call selects there, else select_block_kernel up to 8,192 candidates, select_kernel up to
+    12,288 and select_stream_kernel beyond."""
+    call = "one lkv_select_decode call: " if fused else "lkv_bound_topk + lkv_sparse_decode: "
+    if fused and in_decode:
+        return call + "bound_kernel_mf, sparse_decode_kernel choosing the top K itself, decode_merge_kernel"
+    sel = "select_block_kernel" if n_cand <= 8192 else ("select_kernel" if n_cand <= 12288 else "select_stream_kernel")
+    return call + f"bound_kernel_mf, {sel}, sparse_decode_kernel, decode_merge_kernel"
+
+
 def pmc_traffic() -> dict:
     """Calibrated HBM/fabric bytes per launch, per "<leg>/<kernel>", from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary of the default workload (a counter run cannot time itself)."""
@@ -523,10 +535,7 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
                          "so its selected sets equal the reference's except in near-tie cells (|b_K - b_K+1| <= 1e-5 max(1, |b_K|))",
             "dense_layers": 0, "launch": "eager" if args.eager else "hip_graph",
             "launches_per_layer": 3 if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H)) else 4,
-            "step_kernels": ("one lkv_select_decode call: bound_kernel, sparse_decode_kernel choosing the top K itself, decode_merge_kernel"
-                             if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H)) else
-                             ("one lkv_select_decode call: " if m["fused"] else "lkv_bound_topk + lkv_sparse_decode: ")
-                             + "bound_kernel, select_kernel, sparse_decode_kernel, decode_merge_kernel"),
+            "step_kernels": step_kernels(m["fused"], kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H), n_cand),
             "host_memory": "fine-grained" if args.coherent else "coarse-grained",
         },
         "host_syncs_per_layer": 0,
