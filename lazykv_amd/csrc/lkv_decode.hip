@@ -467,6 +467,50 @@ __device__ __forceinline__ void attend_two(const DecodeArgs& a, const Src& s, in
   process_two<D, MT, G, RawModel<D, MT>, NP>(a, s, block_a, block_b, h, limit, q, r, c, st);
 }
 
+// The selected pairs of an 8-wave int8 instance, four per wave per round: all four records' loads
+// are issued before the first is consumed (the HBM plan gives a wave about four), where the
+// two-per-round loop waits for a second round's loads after consuming its first two. The pairs and
+// the order they are consumed in are the two-per-round loop's, so the results are identical.
+// Blocks of at most 16 tokens (one chunk each). IDS_LDS: the ids are in LDS (a launch that selected
+// them itself), else in global memory; each is read through its own address space (a wait on a
+// generic read drains every load in flight).
+template <int D, int MT, int G, int NW, bool IDS_LDS>
+__device__ __forceinline__ void attend_selected_i8_four(const DecodeArgs& a, const int32_t* idx_h, int sel_base, int js, int je,
+                                                        int wave, int h, const float (&q)[G][Lanes<D>::EPL], int r, int c,
+                                                        WaveState<D, G>& st) {
+  using L = Lanes<D>;
+  const Src& s = a.sel;
+  const int nit = min(L::NI, (a.bs + L::RG - 1) / L::RG);
+  // No vector-memory write pending on entry or at the back edge (rows that no consumer reads, of
+  // the pairs attended before, included): the wait analysis otherwise orders each pair's loads
+  // behind the previous pair's. vmcnt(0), with expcnt and lgkmcnt left at their maximum.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  for (int j = js + wave; j < je; j += 4 * NW) {
+    int b[4];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int jj = j + u * NW;
+      if constexpr (IDS_LDS) {
+        b[u] = jj < je ? ((const __attribute__((address_space(3))) int32_t*)idx_h)[jj - sel_base] : -1;
+      } else {
+        b[u] = jj < je ? *gmem<int32_t>(idx_h + (jj - sel_base)) : -1;
+      }
+      ok[u] = b[u] >= 0 && (int64_t)b[u] < s.nblk;
+    }
+    RawI8<D> w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_pair_raw<D, MT>(s, a.bs, ok[u], b[u], h, 0, nit, a.bs, r, c, w[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (ok[u]) finish_raw(0, r, w[u]);  // wave-uniform branches: every lane shuffles
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (ok[u]) consume_chunk<D, G>(q, WidenI8<D, MT>(w[u]), w[u], 0, nit, a.bs, r, st);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  }
+}
+
 // ---- Q.K on the matrix cores ---------------------------------------------------------------------
 // The 8-wave model-dtype instances score a 16-token chunk with one v_mfma_f32_16x16x32 per 32
 // channels: A = the chunk's 16 key rows (lane l: row l % 16, channels 32s + 8 (l / 16) .. + 7),
@@ -890,7 +934,14 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       // 16-row chunks).
       constexpr bool HYB = I8 && NT == kThreads && SEL == 0;
       constexpr int NPA = ((I8 && NT == kThreads) || MT == LKV_F32) ? 1 : 2;
-      for (int j = js + wave; j < je; j += NPA * NW) {
+      bool piped = false;  // the selected pairs were attended four per round
+      if constexpr (I8 && NT == kThreadsHbm && NPA == 2) {
+        if (a.sel.dtype == LKV_INT8_RECORD && a.bs <= 16) {
+          attend_selected_i8_four<D, MT, G, NW, (SEL > 0)>(a, idx_h, sel_base, js, je, wave, h, q, r, c, st);
+          piped = true;
+        }
+      }
+      for (int j = js + wave; j < je && !piped; j += NPA * NW) {
         const int b0 = idx_h[j - sel_base];
         if constexpr (HYB) {
           if (a.loc != nullptr) {  // hybrid residency (one pair per wave per round)
