@@ -405,8 +405,8 @@ __device__ __forceinline__ void consume_chunk(const float (&q)[G][Lanes<D>::EPL]
 
 // Pairs a wave keeps in flight in the remainder segment of the vector-path instances: one
 // (measured on runs of consecutive blocks from HBM and from host memory, two were no faster). The
-// selected segment takes two in the 8-wave int8 instances, one in the 4-wave general instance; the
-// matrix-core instances take up to three in both segments.
+// selected segment takes two in the 8-wave instances (four for int8 records), one in the 4-wave
+// general instance; the matrix-core instances take up to three in both segments.
 template <int G>
 constexpr int kPairs = 1;
 
@@ -925,10 +925,10 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       const int js = max(first, has_sink) - has_sink;
       const int je = min(last, has_sink + n_sel) - has_sink;
       // The hybrid branch is compiled only into the 4-wave general instance, which every hybrid
-      // launch takes. The 8-wave vector-path instances keep two selected pairs in flight per wave:
-      // with about two items per wave in the HBM plan, both loads are issued before either is
-      // consumed (int8 records in HBM 24.4 -> 23.5 us, identical results). Float32 pools keep one
-      // (two would spill).
+      // launch takes. The 8-wave vector-path instances keep two selected pairs in flight per wave
+      // (int8 records in HBM 24.4 -> 23.5 us, identical results), and int8 records of blocks of
+      // at most 16 tokens four (attend_selected_i8_four), in the same order. Float32 pools keep
+      // one (two would spill).
       // A fused-selection instance keeps the pairing of the instance it stands in for, so that both
       // fold each wave's chunks in the same order (with two pairs in flight a wave interleaves their
       // 16-row chunks).
