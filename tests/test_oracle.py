@@ -166,6 +166,30 @@ def test_bound_matches_quests_definition() -> None:
     assert np.allclose(R.quest_bound(q, kmin, kmax, "f32"), R.quest_bound_bruteforce(q, kmin, kmax), atol=1e-4)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_model_dtype_bound_rounds_where_torch_does(dt: str) -> None:
+    """The `dtype=None` bound of lazykv/selection.py:47-52 is two model-dtype matrix products
+    (float32 sums, rounded to the model dtype) and a model-dtype add. torch's own bf16 / fp16
+    kernels evaluate that expression here, on inputs that are multiples of 1/8, so every float32
+    sum is exact and only the rounding points can differ: the oracle's "model" bound must equal
+    it bit for bit, and a single rounding of a + b must not."""
+    import torch
+
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16}[dt]
+    rng = np.random.default_rng(7)
+    h, g, n, d = 2, 4, 300, 32
+    q = rng.integers(-40, 41, (h * g, d)) / 8.0
+    lo = rng.integers(-40, 41, (h, n, d)) / 8.0
+    hi = lo + rng.integers(0, 41, (h, n, d)) / 8.0
+    tq = torch.tensor(q, dtype=tdt).view(1, h, g, d)
+    qp = tq.clamp_min(0)
+    tmin, tmax = torch.tensor(lo, dtype=tdt).view(1, h, n, d), torch.tensor(hi, dtype=tdt).view(1, h, n, d)
+    want = ((qp @ tmax.transpose(-1, -2)) + ((tq - qp) @ tmin.transpose(-1, -2))).amax(dim=2)[0].float().numpy()
+    assert np.array_equal(R.quest_bound(q, lo, hi, "model", dt), want)
+    once = R.round_to(R.quest_bound(q, lo, hi, "f32"), dt)
+    assert not np.array_equal(once, want)
+
+
 def test_bound_dominates_every_dot_product_in_its_block() -> None:
     """tests/test_selection.py:47-56."""
     rng = np.random.default_rng(4)
