@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY. Nothing in `lazykv_amd/` imports, calls or links anything here: the
 product path runs the HIP kernels and fails loudly when they are missing. Only `tests/`,
 `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` use this package, and only
-as the checker (or, for `cpu_path`, as the timed CPU baseline).
+as the reference results are compared against (or, for `cpu_path`, as the timed CPU baseline).
 
 Modules:
 

@@ -49,7 +49,7 @@ def test_record_width_formula_matches_the_reference_fixture() -> None:
     g = np.load(GOLDEN)
     for bs, d, p in g["packed_pair_bytes"]:
         assert R.packed_pair_bytes(int(bs), int(d)) == p
-    # The geometries the workloads use (SURVEY record sizes): P(16,64), P(16,128).
+    # The record sizes of the workloads' geometries: P(16,64), P(16,128).
     assert R.packed_pair_bytes(16, 64) == 2368 and R.packed_pair_bytes(16, 128) == 4672
 
 
