@@ -174,7 +174,7 @@ def verify_strategies(n_q_heads: int, n_kv_heads: int, head_dim: int, dtype: tor
         if name in STRATEGIES:
             checks.append(_verify_hip(n_q_heads, n_kv_heads, head_dim, dtype, probe_ctx, steps, tolerance))
         else:
-            checks.append(KernelCheck(name, False, None, None, None, None, f"unknown strategy {name!r}: this build has {STRATEGIES}"))
+            checks.append(KernelCheck(name, False, None, None, None, None, f"unknown strategy {name!r}: this library has {STRATEGIES}"))
     return checks
 
 
@@ -183,7 +183,7 @@ def install(strategy: str | None = None, n_q_heads: int | None = None, n_kv_head
     """Register the attention function with transformers under IMPLEMENTATION_NAME and pin the
     strategy (lazykv/attention.py:269-290). Given the model's head counts and head_dim, the
     decode kernel and the chunked-prefill path are verified first against a float64 truth; a
-    strategy that fails (or that this build does not have) is a hard error, never a silent
+    strategy that fails (or that this library does not have) is a hard error, never a silent
     fallback."""
     from transformers import AttentionInterface
 
@@ -194,7 +194,7 @@ def install(strategy: str | None = None, n_q_heads: int | None = None, n_kv_head
         if not checks[0].ok:
             raise RuntimeError(f"attention strategy {chosen!r} failed verification: {checks[0]}")
     elif chosen not in STRATEGIES:
-        raise RuntimeError(f"unknown attention strategy {chosen!r}: this build has {STRATEGIES}")
+        raise RuntimeError(f"unknown attention strategy {chosen!r}: this library has {STRATEGIES}")
     _STRATEGY["name"], _STRATEGY["bucket"] = chosen, bucket
     AttentionInterface.register(IMPLEMENTATION_NAME, lazykv_attention_forward)
     return chosen, checks

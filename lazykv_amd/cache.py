@@ -2,7 +2,7 @@
 
 The transformers `Cache` surface of the reference's dense store (`FullGPUCache`, its per-layer
 `PreallocatedLayer` and `CacheStats`, lazykv/cache.py:20-115) is kept, because `TieredCache`,
-`QuestView` and the snapshot reader take one. The storage is laid out for this build:
+`QuestView` and the snapshot reader take one. The storage is laid out for this library:
 
 * A layer's keys and values share one slab `[2, 1, h, capacity, d]` in HBM (`keys` is slab[0],
   `values` slab[1]): one allocation per layer, made the first time the layer sees KV, so a layer

@@ -17,7 +17,7 @@ How each function is pinned (each check lives in `tests/test_oracle.py`):
 * `quest_bound`: brute force of Quest's definition sum_i max(q_i m_i, q_i M_i) (a different
   formula from q+.M + q-.m, so a sign or operand swap fails), the dominance invariant
   (`tests/test_selection.py:47-56`) and the bf16 tie known answer (`tests/test_selection.py:121-133`).
-* `top_blocks`: brute-force sort; tie order (lower block id first) is this build's rule.
+* `top_blocks`: brute-force sort; tie order (lower block id first) is the rule of lkv_bound_topk.
 * `block_minmax`, `current_block_mask`, `blocks_for_budget`: closed forms and the reference's
   own known answers (`tests/test_selection.py:38-44,98`).
 * `residency_step`: invariants that fix it (after a step the resident set is exactly the chosen

@@ -609,7 +609,7 @@ def test_pinned_pool_round_trips_and_the_stream_probe_reads_it() -> None:
 def test_install_verifies_the_decode_kernel_and_refuses_unknown_strategies() -> None:
     """install() with the model's head counts checks decode (the HIP kernel, spare storage past the
     live length) and chunked prefill against a float64 truth first (lazykv/attention.py:214-290);
-    a strategy this build does not have is a hard error."""
+    a strategy this library does not have is a hard error."""
     from lazykv_amd import attention
 
     chosen, checks = attention.install(None, 32, 8, 128)
@@ -631,7 +631,7 @@ def test_attention_seam_refuses_a_mask_and_reads_only_the_live_prefix() -> None:
     whose spare rows hold large values matches the float64 truth within 1e-2 relative, for a decode
     token and for a 17-token chunk. head_dim is 64, the smallest the decode kernel takes (the
     reference's test uses 16). The startup verification passes for the build's strategy and fails,
-    without raising, for one the build does not have (lazykv/attention.py:248-266)."""
+    without raising, for one the library does not have (lazykv/attention.py:248-266)."""
     from lazykv_amd.attention import _truth, attend, lazykv_attention_forward, verify_strategies
 
     q = torch.randn(1, 8, 1, 64, device="cuda", dtype=torch.float16)

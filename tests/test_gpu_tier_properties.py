@@ -1,4 +1,4 @@
-"""Properties of the host tier that the reference's own tests state, restated for this build (GPU):
+"""Properties of the host tier that the reference's own tests state, restated for the tiered cache here (GPU):
 exact-size pinning outside torch's caching host allocator (tests/test_pinned.py:12-40), the int8
 host pool narrowing by exactly the record width and the sink staying exact
 (tests/test_tiered_int8.py:27-99), `pack` keeping the leading axes (tests/test_quant.py:29-34), and
@@ -67,7 +67,7 @@ def test_the_int8_host_pool_narrows_by_exactly_the_record_width_and_the_sink_sta
     torch.cuda.synchronize()
     assert exact.n_sealed == narrow.n_sealed == 40
     assert narrow.host_bytes() * (2 * BS * D * 2) == exact.host_bytes() * packed_pair_bytes(BS, D)
-    # Block 0 never leaves the GPU pool, so it is not narrowed (lazykv/tiered.py:200-202).
+    # Block 0 never leaves HBM, so it is not narrowed (lazykv/tiered.py:200-202).
     assert torch.equal(narrow.pool[0, :, 0].cpu(), keys[0, :, :BS])
     assert torch.equal(narrow.pool[0, :, 1].cpu(), values[0, :, :BS])
 
