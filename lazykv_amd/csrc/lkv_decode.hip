@@ -1056,7 +1056,9 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
 // Folds the S partials of one query head into its output and LSE. One 512-thread workgroup per
 // query head; thread t owns channel t % D of partial rows t / D, t / D + 512 / D, ... Every load
 // of a round (the partial outputs and the (m, l) pairs) is issued before any is used, so for
-// S <= 16 * 512 / D partials the merge is one memory round trip.
+// S <= 16 * 512 / D partials the merge is one memory round trip. Workgroup b takes KV head
+// b % n_kv, as the decode launch's workgroups do, so the merge of a head runs on the XCD whose
+// L2 its partials were written through.
 template <int D, int G>
 __global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_o,
                                                            int S, void* __restrict__ out, int out_dtype,
@@ -1064,8 +1066,9 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restri
   constexpr int kT = 512;
   constexpr int kSlices = kT / D;  // partial rows read side by side
   constexpr int kU = 16;           // partial rows per thread per round
-  const int row = blockIdx.x;      // query head h * G + j
-  const int h = row / G, j = row % G;
+  const int n_kv = gridDim.x / G;
+  const int h = blockIdx.x % n_kv, j = blockIdx.x / n_kv;
+  const int row = h * G + j;  // query head
   const int t = threadIdx.x;
   const int d = t % D, slice = t / D;
   const float* ml = part_ml + (int64_t)h * S * G * 2;
