@@ -584,27 +584,29 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
 
     # ---- CPU baseline: the reference's path for this workload on this host's cores ---------------
     if not args.no_cpu_baseline:
-        last = list(res.values())[-1]
-        # Layer 0 decoded once more by the main leg's kernels, with a float32 output, for the
-        # parity figure beside the timing (the timed steps write the model dtype).
+        # Layer 0 decoded once more by the main leg's kernels, with a float32 output for the parity
+        # figure beside the timing, and with the model-dtype output the timed steps write (not the
+        # last leg's layer 0: in the reference's 2-dense variant that layer is dense).
         name0, k0, sels0, rems0 = legs[0]
         st0 = layers[0]
         ss0 = kernels.pool_source(st0["slots"])
-        if res[name0]["fused"]:
-            f32 = kernels.select_decode(st0["q"], st0["kmin"], st0["kmax"], k0, cand_offset=1, n_cand=n_cand, block_size=BS, scale=scale, sel=sels0[0],
-                                        sink=ss0, sink_block=0, cur=ss0, cur_block=1, fill=fill, out_dtype=torch.float32)
-        else:
+
+        def layer0(out_dtype: torch.dtype) -> tuple:
+            if res[name0]["fused"]:
+                return kernels.select_decode(st0["q"], st0["kmin"], st0["kmax"], k0, cand_offset=1, n_cand=n_cand, block_size=BS, scale=scale, sel=sels0[0],
+                                             sink=ss0, sink_block=0, cur=ss0, cur_block=1, fill=fill, out_dtype=out_dtype)
             idx0 = kernels.bound_topk(st0["q"], st0["kmin"], st0["kmax"], k0, cand_offset=1, n_cand=n_cand)
             extra0 = dict(rem=rems0[0], rem_range=(1, n_sealed)) if rems0 is not None else {}
-            f32 = kernels.sparse_decode(st0["q"], n_kv=H, block_size=BS, scale=scale, sel=sels0[0], idx=idx0, sink=ss0, sink_block=0, cur=ss0, cur_block=1,
-                                        fill=fill, out_dtype=torch.float32, **extra0)
+            return kernels.sparse_decode(st0["q"], n_kv=H, block_size=BS, scale=scale, sel=sels0[0], idx=idx0, sink=ss0, sink_block=0, cur=ss0, cur_block=1,
+                                         fill=fill, out_dtype=out_dtype, **extra0)
+
+        f32, md = layer0(torch.float32), layer0(st0["slots"].dtype)
         torch.cuda.synchronize()
-        out["cpu_baseline"] = cpu_baseline_decode(kind, layers, ks[0], n_sealed, fill, scale, args.cpu_seconds, outs, last, (name0, k0, f32))
+        out["cpu_baseline"] = cpu_baseline_decode(kind, layers, ks[0], n_sealed, fill, scale, args.cpu_seconds, (name0, k0, f32, md))
     return out
 
 
-def cpu_baseline_decode(kind: str, layers: list, k: int, n_sealed: int, fill: int, scale: float, budget_s: float, outs: list, last_leg: dict,
-                        f32_layer0: tuple | None = None) -> dict:
+def cpu_baseline_decode(kind: str, layers: list, k: int, n_sealed: int, fill: int, scale: float, budget_s: float, layer0: tuple) -> dict:
     from oracle import cpu_path
 
     n_layers = min(len(layers), 2 if kind == "exact" else 8)
@@ -632,14 +634,13 @@ def cpu_baseline_decode(kind: str, layers: list, k: int, n_sealed: int, fill: in
     # float32-output decode is the figure held to the 2e-3 bar; the timed model-dtype output also
     # carries its own rounding (one step of the output dtype, 2^-8 of |out| for bfloat16).
     r0 = fn(*states[0])
-    diff = float((r0[0] - outs[0].float().cpu()).abs().max()) if last_leg["k"] == k else None
-    parity = {}
-    if f32_layer0 is not None:
-        leg, k0, (o32, l32) = f32_layer0
-        if k0 == k:
-            parity = {"gpu_vs_cpu_layer0_max_abs_out_f32": float((r0[0] - o32.cpu()).abs().max()),
-                      "gpu_vs_cpu_layer0_max_abs_lse": float((r0[1] - l32.cpu()).abs().max()),
-                      "parity_leg": leg, "parity_bar": 2e-3}
+    leg, k0, (o32, l32), (omd, _) = layer0
+    parity, diff = {}, None
+    if k0 == k:
+        parity = {"gpu_vs_cpu_layer0_max_abs_out_f32": float((r0[0] - o32.cpu()).abs().max()),
+                  "gpu_vs_cpu_layer0_max_abs_lse": float((r0[1] - l32.cpu()).abs().max()),
+                  "parity_leg": leg, "parity_bar": 2e-3}
+        diff = float((r0[0] - omd.float().cpu()).abs().max())
     t = time_cpu(fn, states, budget_s)
     samples = {"host": "single-layer decodes: fp32 quest bound, topk, index_select gather from the host pool, cat, masked fp32 attention + logsumexp",
                "hbm": "single-layer decodes: fp32 quest bound, topk, index_select gather, cat, masked fp32 attention + logsumexp",
