@@ -143,13 +143,23 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const
 #ifndef LKV_DECODE_NT
 #define LKV_DECODE_NT 1
 #endif
-template <typename T>
-__device__ __forceinline__ T load_kv(const void* p) {
-#if LKV_DECODE_NT
-  return __builtin_nontemporal_load(gmem<T>(p));
-#else
-  return *gmem<T>(p);
+// Either half alone is slower than both (the 8B-shaped step in HBM: 30.70 us per layer with both,
+// 31.18 with ordinary key-row loads in the matrix-core instances, 31.78 with ordinary loads
+// elsewhere; A/B over three rounds), although the streamed key rows raise that step's fetched
+// bytes from 1.03x to 1.06x of the pairs'.
+#ifndef LKV_DECODE_NT_MFK
+#define LKV_DECODE_NT_MFK 1  // the matrix-core instances' key-row loads
 #endif
+#ifndef LKV_DECODE_NT_WORDS
+#define LKV_DECODE_NT_WORDS 1  // every other pair load (value rows, vector and int8 key rows, scales)
+#endif
+template <typename T, bool NT = (LKV_DECODE_NT && LKV_DECODE_NT_WORDS)>
+__device__ __forceinline__ T load_kv(const void* p) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(gmem<T>(p));
+  } else {
+    return *gmem<T>(p);
+  }
 }
 
 template <int W>
@@ -591,7 +601,7 @@ __device__ __forceinline__ void load_raw_mf(const Src& s, int block, int h, int 
   const int kr = t0 + lane % 16;
   const uint16_t* krow = kb + (int64_t)(kr < limit ? kr : 0) * D + 8 * (lane / 16);
 #pragma unroll
-  for (int st = 0; st < D / 32; ++st) raw.k[st] = __builtin_bit_cast(typename Mfma<MT>::V8, load_kv<u32x4>(krow + 32 * st));
+  for (int st = 0; st < D / 32; ++st) raw.k[st] = __builtin_bit_cast(typename Mfma<MT>::V8, load_kv<u32x4, (LKV_DECODE_NT && LKV_DECODE_NT_MFK)>(krow + 32 * st));
 #pragma unroll
   for (int i = 0; i < L::NI; ++i) {
     const int row = t0 + r + L::RG * i;
