@@ -814,7 +814,7 @@ def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
     log(f"model and pools ready in {time.time() - t0:.1f}s")
     runs = []
     for i in range(args.warmup + reps):
-        r = tiered_prefill(model, ids, chunk, k, BS, cap, dense_layers=0, host_pools=pools, quant="int8")
+        r = tiered_prefill(model, ids, chunk, k, BS, cap, dense_layers=0, host_pools=pools, quant="int8", fetch="zerocopy")
         if i >= args.warmup:
             runs.append((r.wall_s, r.boundary_layer_s, r.chunks))
         del r
@@ -829,7 +829,7 @@ def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
             full = FullGPUCache(L, cap)
             for s in range(0, n, chunk):
                 model(input_ids=ids[:, s : s + chunk], past_key_values=full, use_cache=True, logits_to_keep=1)
-            cache = TieredCache(full, k, BS, cap, dense_layers=0, host_pools=pools, quant="int8")
+            cache = TieredCache(full, k, BS, cap, dense_layers=0, host_pools=pools, quant="int8", fetch="zerocopy")
         torch.cuda.synchronize()
         if i >= args.warmup:
             ref_walls.append(time.perf_counter() - w0)

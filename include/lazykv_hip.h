@@ -171,25 +171,43 @@ int lkv_sparse_decode_static(uintptr_t stream, const lkv_decode_desc* desc, cons
 /* ---- next row: device-side hybrid residency. Replaces rung 6's host-side admit / gather
  * (lazykv/tiered.py:389-487: the least recently used slots outside the chosen set are the victims,
  * lazykv/tiered.py:397-418) with device work and no host sync. The reference itself never combined
- * residency with the zero-copy read. Per KV head, `slots` holds k slots of pairs in HBM; the
- * tables block_slot[h * block_slot_stride + b] (slot or -1) and slot_block[h * slot_block_stride +
- * s] (block or -1) say which blocks they hold; the caller allocates them on the device and fills
- * them with -1 once. A block counts as resident only where both tables agree, so tables left
- * inconsistent (or filled with zeros) cost misses, not wrong reads. Each call first updates the
- * tables for the selection idx: with as many slots
- * as selected blocks, the slots the selection does not hit are exactly the victims, taken in
- * ascending slot order by the missed blocks in ascending block order. It then attends as
- * lkv_sparse_decode does over `host` (mapped host memory: model-dtype pairs, or int8 records as in
- * rung 8, lazykv/tiered.py:182-196): a hit is read from its slot in HBM; a miss is read from `host`
- * and its pair -- for int8 records, the dequantised model-dtype rows -- written into its new slot on
- * the way. `slots` holds the model dtype. The output and LSE equal lkv_sparse_decode's over `host`
- * bit for bit; only where the bytes come from differs. desc->k <= 4096, no remainder. */
+ * residency with the zero-copy read. Per KV head, `slots` holds slots->n_blocks = n_slots >= k slots
+ * of pairs in HBM (the reference's n_slots: k selected blocks plus spare ones,
+ * lazykv/tiered.py:247-252, lazykv/sweep.py:120-125), at most 4,096. The tables of lkv_residency say
+ * which blocks they hold: block_slot[h * block_slot_stride + b] (slot or -1) and
+ * slot_block[h * slot_block_stride + s] (block or -1); the caller allocates them on the device and
+ * fills them with -1 once (or with a seeded residency). A block counts as resident only where both
+ * tables agree, so tables left inconsistent (or filled with zeros) cost misses, not wrong reads.
+ * order[h * order_stride + 0 .. n_slots) lists the head's slots from least to most recently used
+ * (empty slots first); it is required when n_slots > k (start it as 0, 1, ..., n_slots - 1, or with
+ * the empty slots ahead of seeded ones) and may be NULL when n_slots == k, where every unhit slot is
+ * a victim anyway. An order that is not a permutation of the slots is read as ascending slot order.
+ * Each call first updates the tables for the selection idx: the victims are the slots the selection
+ * does not hit, least recently used first, as many as it misses, and they go to the missed blocks in
+ * ascending block order; the slots the step used (hits and victims) move to the end of the order in
+ * ascending slot order. It then attends as lkv_sparse_decode does over `host` (mapped host memory:
+ * model-dtype pairs, or int8 records as in rung 8, lazykv/tiered.py:182-196): a hit is read from its
+ * slot in HBM; a miss is read from `host` and its pair -- for int8 records, the dequantised
+ * model-dtype rows -- written into its new slot on the way. `slots` holds the model dtype. `rem`, if
+ * desc->rem_last > desc->rem_first, is the exact tier's remainder, as in lkv_sparse_decode: every
+ * block of the range the selection does not name, attended from `rem` and merged by log-sum-exp
+ * (rung 9 over rung 6's residency, lazykv/exact.py:155-264). The output and LSE equal
+ * lkv_sparse_decode's over `host` (and `rem`) bit for bit; only where the bytes come from differs.
+ * desc->k <= n_slots <= 4096. */
+typedef struct lkv_residency {
+  int32_t* block_slot;
+  int64_t block_slot_stride;
+  int32_t* slot_block;
+  int64_t slot_block_stride;
+  int32_t* order;
+  int64_t order_stride;
+} lkv_residency;
+
 size_t lkv_hybrid_decode_workspace_bytes(const lkv_decode_desc* desc);
 int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
                       const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* idx, int64_t idx_stride,
-                      int32_t* block_slot, int64_t block_slot_stride, int32_t* slot_block, int64_t slot_block_stride,
-                      const lkv_kv_source* sink, const lkv_kv_source* cur, void* out, int out_dtype, float* lse,
-                      void* ws, size_t ws_bytes);
+                      const lkv_residency* res, const lkv_kv_source* sink, const lkv_kv_source* cur,
+                      const lkv_kv_source* rem, void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes);
 
 /* ---- a1 + a2 + f3 + a6: one selecting layer's hybrid decode step
  * (lazykv/tiered.py:383-387 rank + :389-487 the hybrid fetch + lazykv/attention.py:97-136 attend;
@@ -200,14 +218,15 @@ int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void*
  * selection takes a launch of its own), so the step is four launches instead of five. The ids,
  * the tables after the call, the output and the LSE equal lkv_bound_topk followed by
  * lkv_hybrid_decode, bit for bit. out_idx, if not NULL, receives the selected ids in ascending
- * order (idx_stride apart per head). Arguments as in those two calls. */
+ * order (idx_stride apart per head). Arguments as in those two calls; `rem` as in
+ * lkv_hybrid_decode (the exact tier's remainder, excluding the ids this call selects). */
 size_t lkv_select_hybrid_decode_workspace_bytes(const lkv_decode_desc* desc, int n_cand);
 int lkv_select_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype, const void* kmin,
                              const void* kmax, int meta_dtype, int64_t meta_head_stride, int cand_offset, int n_cand,
-                             int rank_mode, const lkv_kv_source* host, const lkv_kv_source* slots, int32_t* block_slot,
-                             int64_t block_slot_stride, int32_t* slot_block, int64_t slot_block_stride,
-                             const lkv_kv_source* sink, const lkv_kv_source* cur, void* out, int out_dtype, float* lse,
-                             int32_t* out_idx, int64_t idx_stride, void* ws, size_t ws_bytes);
+                             int rank_mode, const lkv_kv_source* host, const lkv_kv_source* slots,
+                             const lkv_residency* res, const lkv_kv_source* sink, const lkv_kv_source* cur,
+                             const lkv_kv_source* rem, void* out, int out_dtype, float* lse, int32_t* out_idx,
+                             int64_t idx_stride, void* ws, size_t ws_bytes);
 
 /* ---- a8: exact two-partial merge (lazykv/exact.py:69-85 merge_lse)
  * rows x d outputs (dtype_in) and their LSEs; an empty partial (lse -inf) contributes 0.

@@ -24,11 +24,23 @@ SRC_HOST = 1
 SELECT_IN_DECODE_MAX_CAND = 8192  # lkv_select_decode chooses the top K inside the decode launch up to this many candidates
 
 
-def selects_in_decode(n_cand: int, host: bool, group: int) -> bool:
-    """Whether lkv_select_decode chooses the top K inside its decode launch, as the library decides:
-    up to 16 candidates per thread of that launch -- 512 threads when the selected pairs are in HBM
-    and the query group is at most 4, else 256 -- and never beyond SELECT_IN_DECODE_MAX_CAND."""
-    threads = 512 if (not host and group <= 4) else 256
+def selects_in_decode(n_cand: int, host: bool, group: int, int8: bool = False, head_dim: int = 128, model_query: bool = True) -> bool:
+    """Whether lkv_select_decode chooses the top K inside its decode launch, as the library decides.
+    The decode launch must take the instance the unfused decode takes, and hold at most 16 candidates
+    per thread, never beyond SELECT_IN_DECODE_MAX_CAND. Pairs in HBM with a query group of at most 4
+    take 512-thread workgroups: matrix-core ones for a model-dtype query (`model_query`: the pools'
+    dtype, 16-byte aligned), int8-capable ones for int8 records (except head_dim 128 with a group of
+    4, which takes 256); an HBM launch with any other query has no selecting instance of its own and
+    selects in its own launch. Everything else takes 256 threads."""
+    if not host and group <= 4:
+        if int8:
+            threads = 256 if (head_dim == 128 and group == 4) else 512
+        elif model_query:
+            threads = 512
+        else:
+            return False
+    else:
+        threads = 256
     return n_cand <= min(SELECT_IN_DECODE_MAX_CAND, 16 * threads)
 
 
@@ -78,6 +90,19 @@ class DecodeDesc(ctypes.Structure):
     ]
 
 
+class ResidencyTables(ctypes.Structure):
+    """lkv_residency: a hybrid tier's tables (which block each HBM slot holds, and their use order)."""
+
+    _fields_ = [
+        ("block_slot", ctypes.c_void_p),
+        ("block_slot_stride", ctypes.c_int64),
+        ("slot_block", ctypes.c_void_p),
+        ("slot_block_stride", ctypes.c_int64),
+        ("order", ctypes.c_void_p),
+        ("order_stride", ctypes.c_int64),
+    ]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
@@ -113,14 +138,15 @@ SIGNATURES: dict[str, tuple] = {
     "lkv_hybrid_decode_workspace_bytes": (_SZ, [ctypes.POINTER(DecodeDesc)]),
     "lkv_hybrid_decode": (
         _I,
-        [_U, ctypes.POINTER(DecodeDesc), _P, _I, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I64, _P, _I64, _P, _I64,
-         ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I, _P, _P, _SZ],
+        [_U, ctypes.POINTER(DecodeDesc), _P, _I, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I64,
+         ctypes.POINTER(ResidencyTables), ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I, _P, _P, _SZ],
     ),
     "lkv_select_hybrid_decode_workspace_bytes": (_SZ, [ctypes.POINTER(DecodeDesc), _I]),
     "lkv_select_hybrid_decode": (
         _I,
         [_U, ctypes.POINTER(DecodeDesc), _P, _I, _P, _P, _I, _I64, _I, _I, _I, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource),
-         _P, _I64, _P, _I64, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I, _P, _P, _I64, _P, _SZ],
+         ctypes.POINTER(ResidencyTables), ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _P, _I, _P, _P,
+         _I64, _P, _SZ],
     ),
     "lkv_merge_lse": (_I, [_U, _P, _P, _P, _P, _I, _I64, _I, _P, _I, _P]),
     "lkv_store_blocks": (_I, [_U, ctypes.POINTER(KVSource), ctypes.POINTER(KVSource), _I, _I, _I, _I, _I, _P, _P, _I, _I64]),

@@ -14,26 +14,42 @@ scaled_dot_product_attention with the reference's lower-right causal alignment.
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
+from collections.abc import Callable
+from dataclasses import dataclass, replace
 
 import torch
 
 from lazykv_amd import kernels
 
 IMPLEMENTATION_NAME = "lazykv_sdpa"
+DEFAULT_BUCKET = 1024  # the reference's bucket default (:42); the decode kernel has no use for one
 DENSE_BLOCK = 16  # block granularity the dense decode walks the cache in
-STRATEGIES = ("hip",)  # the decode kernel; the reference's are cuDNN / SDPA backends (:44)
-_STRATEGY = {"name": "hip", "bucket": 0}
+# The reference's names pick a cuDNN or SDPA backend (lazykv/attention.py:44,104-113). This library
+# has one decode implementation, the HIP kernel, so every one of those names selects it: a caller
+# that installs "cudnn_bucketed" (as the reference's fixtures and generate.py do) registers the HIP
+# path and has it verified. "hip" names it directly.
+REFERENCE_STRATEGIES = ("cudnn_bucketed", "cudnn", "efficient", "math")
+STRATEGIES = ("hip",) + REFERENCE_STRATEGIES
+_STRATEGY = {"name": "hip", "bucket": DEFAULT_BUCKET}
 
 
-def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float | None, strategy: str = "hip", bucket: int = 0, mask: torch.Tensor | None = None) -> torch.Tensor:
+def _known(strategy: str) -> None:
+    if strategy not in STRATEGIES:
+        raise ValueError(f"unknown attention strategy {strategy!r}; this library has {STRATEGIES}")
+
+
+def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float | None, strategy: str = "hip", bucket: int = DEFAULT_BUCKET, mask: torch.Tensor | None = None) -> torch.Tensor:
     """Exact attention of `query` [1, n_q, q_len, d] over all of `key`/`value` [1, kv, L, d].
 
     Decode (q_len 1) runs the HIP decode kernel over the L tokens (whole blocks from the cache
     plus a partial last block). `mask`, if given, must be the current-block mask of
-    lazykv/selection.py:65-69; the kernel needs only its count of live positions.
+    lazykv/selection.py:65-69; the kernel needs only its count of live positions. Every name in
+    STRATEGIES selects this path; another name is a ValueError, as in the reference (:113). `bucket`
+    is accepted for the reference's signature: the kernel reads exactly the live prefix, so there is
+    no plan to keep stable across lengths and nothing to pad.
     """
-    del strategy, bucket
+    _known(strategy)
+    del bucket
     q_len, kv_len, d = query.shape[-2], key.shape[-2], query.shape[-1]
     scale = scaling if scaling is not None else d**-0.5
     if q_len > 1:
@@ -167,37 +183,60 @@ def _verify_hip(n_q: int, n_kv: int, head_dim: int, dtype: torch.dtype, probe_ct
 def verify_strategies(n_q_heads: int, n_kv_heads: int, head_dim: int, dtype: torch.dtype = torch.bfloat16, tolerance: float = 1e-2,
                       probe_ctx: int = 16_000, steps: int = 24, candidates: tuple[str, ...] = STRATEGIES) -> list[KernelCheck]:
     """Correctness of decode and chunked prefill, and growing-length decode speed, for each
-    candidate strategy (the reference's entry point, lazykv/attention.py:248-266). A strategy this
-    build does not have fails its check instead of raising."""
+    candidate strategy (the reference's entry point, lazykv/attention.py:248-266). The names in
+    STRATEGIES all select the HIP kernel, which is checked once and reported under each of them; a
+    name this library does not have fails its check instead of raising."""
     checks = []
+    measured: KernelCheck | None = None
     for name in candidates:
-        if name in STRATEGIES:
-            checks.append(_verify_hip(n_q_heads, n_kv_heads, head_dim, dtype, probe_ctx, steps, tolerance))
-        else:
+        if name not in STRATEGIES:
             checks.append(KernelCheck(name, False, None, None, None, None, f"unknown strategy {name!r}: this library has {STRATEGIES}"))
+            continue
+        if measured is None:
+            measured = _verify_hip(n_q_heads, n_kv_heads, head_dim, dtype, probe_ctx, steps, tolerance)
+        checks.append(replace(measured, strategy=name))
     return checks
 
 
 def install(strategy: str | None = None, n_q_heads: int | None = None, n_kv_heads: int | None = None, head_dim: int | None = None,
-            bucket: int = 0) -> tuple[str, list[KernelCheck]]:
+            bucket: int = DEFAULT_BUCKET) -> tuple[str, list[KernelCheck]]:
     """Register the attention function with transformers under IMPLEMENTATION_NAME and pin the
-    strategy (lazykv/attention.py:269-290). Given the model's head counts and head_dim, the
-    decode kernel and the chunked-prefill path are verified first against a float64 truth; a
-    strategy that fails (or that this library does not have) is a hard error, never a silent
-    fallback."""
+    strategy (lazykv/attention.py:269-290). Given the model's head counts and head_dim, the decode
+    kernel and the chunked-prefill path are verified first against a float64 truth. A named strategy
+    that fails (or that this library does not have) is a hard error, never a silent fallback.
+    `strategy=None` picks the fastest strategy that verifies; every name is the same HIP kernel, so
+    that is "hip"."""
     from transformers import AttentionInterface
 
     checks: list[KernelCheck] = []
+    if strategy is not None and strategy not in STRATEGIES:
+        # The reference's refusal of a name it did not verify: a RuntimeError (:282-284).
+        raise RuntimeError(f"requested attention strategy {strategy!r} is unknown: this library has {STRATEGIES}")
     chosen = strategy or "hip"
     if n_q_heads is not None and n_kv_heads is not None and head_dim is not None:
         checks = verify_strategies(n_q_heads, n_kv_heads, head_dim, candidates=(chosen,))
         if not checks[0].ok:
-            raise RuntimeError(f"attention strategy {chosen!r} failed verification: {checks[0]}")
-    elif chosen not in STRATEGIES:
-        raise RuntimeError(f"unknown attention strategy {chosen!r}: this library has {STRATEGIES}")
+            what = "no attention strategy passed verification" if strategy is None else f"requested attention strategy {chosen!r} failed verification"
+            raise RuntimeError(f"{what}: {checks[0]}")
     _STRATEGY["name"], _STRATEGY["bucket"] = chosen, bucket
     AttentionInterface.register(IMPLEMENTATION_NAME, lazykv_attention_forward)
     return chosen, checks
+
+
+def set_strategy_for_test(strategy: str) -> Callable[[], None]:
+    """Pin `strategy` for a test or cross-check and register the attention function; returns the
+    function that restores the previous strategy (lazykv/attention.py:301-310)."""
+    from transformers import AttentionInterface
+
+    _known(strategy)
+    previous = _STRATEGY["name"]
+    _STRATEGY["name"] = strategy
+    AttentionInterface.register(IMPLEMENTATION_NAME, lazykv_attention_forward)
+
+    def restore() -> None:
+        _STRATEGY["name"] = previous
+
+    return restore
 
 
 def current_strategy() -> tuple[str, int]:

@@ -17,7 +17,7 @@ void lkv_clear_error() { g_error[0] = '\0'; }
 
 extern "C" const char* lkv_last_error(void) { return g_error; }
 
-extern "C" int lkv_abi_version(void) { return 3; }
+extern "C" int lkv_abi_version(void) { return 4; }
 
 extern "C" int64_t lkv_packed_pair_bytes(int block_size, int head_dim) {
   // lazykv/quant.py:46-49: int8 keys and values, plus float16 k scale/zero per channel and

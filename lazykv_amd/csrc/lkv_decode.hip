@@ -1250,11 +1250,11 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
 // vector path otherwise, int8-capable when a source is int8 records (except D 128 with G 4, which
 // spills there and takes the 4-wave instance over the same plan). Host plans, hybrid launches and
 // groups of 8 take the 4-wave general instance. A fused-selection launch has no 8-wave vector
-// instance and takes the general one instead.
+// instance and takes the general one instead (lkv_select_decode then selects in its own launch, so
+// that it folds what the unfused call folds).
 enum class Inst { kGeneral, kVector8, kInt8x8, kMatrix8 };
 
-template <int D, int MT, int G>
-Inst pick_instance(const DecodeArgs& a, bool sel) {
+static Inst pick_instance(const DecodeArgs& a, int D, int MT, int G, bool sel) {
   const bool i8 = a.sel.dtype == LKV_INT8_RECORD || a.rem.dtype == LKV_INT8_RECORD || a.sink.dtype == LKV_INT8_RECORD ||
                   a.cur.dtype == LKV_INT8_RECORD || a.loc != nullptr;
   if (G > 4 || a.nt != kThreadsHbm || a.loc != nullptr) return Inst::kGeneral;
@@ -1265,6 +1265,9 @@ Inst pick_instance(const DecodeArgs& a, bool sel) {
   }
   return (D == 128 && G == 4) ? Inst::kGeneral : Inst::kInt8x8;
 }
+
+// Threads per workgroup of an instance.
+static int inst_threads(Inst i) { return i == Inst::kGeneral ? kThreads : kThreadsHbm; }
 
 template <int D, int MT, int G, int SEL>
 int launch_inst(hipStream_t stream, DecodeArgs& a, Inst inst) {
@@ -1302,7 +1305,7 @@ template <int D, int MT, int G>
 int launch(hipStream_t stream, DecodeArgs& a) {
   const bool sel = a.bounds != nullptr;
   const int S = a.splits_a + a.splits_b;
-  Inst inst = pick_instance<D, MT, G>(a, sel);
+  Inst inst = pick_instance(a, D, MT, G, sel);
   if ((inst == Inst::kMatrix8 && (MT == LKV_F32 || G > 4)) || (inst == Inst::kInt8x8 && (G > 4 || (D == 128 && G == 4))) ||
       (inst == Inst::kVector8 && (G > 4 || sel)))
     inst = Inst::kGeneral;  // no such instance (pick_instance never asks for one)
@@ -1329,13 +1332,19 @@ int dispatch_g(int g, hipStream_t s, DecodeArgs& a) {
 }
 
 // ---- hybrid residency: which selected blocks are in the HBM slots, and who gets evicted ----------
-// One workgroup per KV head. With as many slots as selected blocks (the reference's default,
-// lazykv/tiered.py:247-250), the victims of a step are exactly the slots its selection does not
-// hit (the least recently used slots outside the chosen set, lazykv/tiered.py:389-418). They are
-// taken in ascending slot order and given to the missed blocks in ascending block order. Tables:
-// block_slot[h][b] = slot or -1, slot_block[h][s] = block or -1. Writes loc[h][j] for the decode:
-// the slot of a hit, kLocMiss | slot for a miss (read from the host, copied into the slot), or -1
-// for an id outside the pool (attended nowhere, like the plain path).
+// One workgroup per KV head, n_slots >= k slots per head. The victims of a step are the least
+// recently used slots outside the chosen set (lazykv/tiered.py:389-418): the slots the selection
+// does not hit, in least-recently-used order, as many as the selection misses, given to the missed
+// blocks in selection order (ascending block ids). `order` lists the head's slots from least to most
+// recently used; a step moves the slots it uses (hits and victims) to the end, in ascending slot
+// order, and keeps the others in their order. That is the reference's stable sort of slots by their
+// last-use step (empty slots first), without a step counter. With as many slots as selected blocks
+// every unhit slot is a victim and the order does not matter: `order` may then be NULL and is read
+// as ascending slot order. An order that is not a permutation of the head's slots is read as
+// ascending slot order too (and rewritten). Tables: block_slot[h][b] = slot or -1, slot_block[h][s]
+// = block or -1. Writes loc[h][j] for the decode: the slot of a hit, kLocMiss | slot for a miss (read
+// from the host, copied into the slot), or -1 for an id outside the pool (attended nowhere, like the
+// plain path).
 constexpr int kResThreads = 1024;  // 1,024 threads: a selecting launch holds 8 keys per thread (16 at 512 were slower)
 constexpr int kMaxSlots = 4096;
 constexpr int kResPer = kMaxSlots / kResThreads;  // items and slots per thread
@@ -1369,13 +1378,24 @@ struct ResSelect {
 constexpr int kResSelKpt = kSelCap / kResThreads;  // candidates per thread of a selecting residency launch
 constexpr int kResCacheBlocks = 8192;               // block_slot rows up to this long are read into LDS
 
+// The residency tables of one call: n_slots slots per head, `order` optional (see above).
+struct ResTables {
+  int32_t* block_slot;
+  int64_t bslot_stride;
+  int64_t n_blocks;
+  int32_t* slot_block;
+  int64_t sblock_stride;
+  int32_t* order;
+  int64_t order_stride;
+  int n_slots;
+};
+
 template <bool SEL>
 __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int k,
-                                                                int32_t* __restrict__ block_slot, int64_t bslot_stride,
-                                                                int64_t n_blocks, int32_t* __restrict__ slot_block,
-                                                                int64_t sblock_stride, int32_t* __restrict__ loc,
-                                                                int64_t loc_stride, ResSelect rs) {
+                                                                ResTables t, int32_t* __restrict__ loc, int64_t loc_stride,
+                                                                ResSelect rs) {
   __shared__ uint32_t hit[kMaxSlots / 32];
+  __shared__ uint32_t used[kMaxSlots / 32];  // hit or taken as a victim this step; first: the order's validity check
   __shared__ int32_t victims[kMaxSlots];
   __shared__ uint32_t scan_a[kResThreads / 64], scan_b[kResThreads / 64];
   using SelLds = typename std::conditional<SEL, lkv::SelectLds<kResThreads, kResSelKpt>, char>::type;
@@ -1383,9 +1403,13 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   __shared__ int32_t s_ids[SEL ? kMaxSlots : 1];
   __shared__ int32_t s_bslot[kResCacheBlocks];
   __shared__ int32_t s_sblock[kMaxSlots];
+  __shared__ int32_t s_order[kMaxSlots];
   const int h = blockIdx.x;
-  int32_t* bslot_h = block_slot + (int64_t)h * bslot_stride;
-  int32_t* sblock_h = slot_block + (int64_t)h * sblock_stride;
+  const int n_slots = t.n_slots;
+  const int64_t n_blocks = t.n_blocks;
+  int32_t* bslot_h = t.block_slot + (int64_t)h * t.bslot_stride;
+  int32_t* sblock_h = t.slot_block + (int64_t)h * t.sblock_stride;
+  int32_t* order_h = t.order != nullptr ? t.order + (int64_t)h * t.order_stride : nullptr;
   // Rows of up to kResCacheBlocks blocks: both tables are read into LDS once, their loads issued
   // ahead of the selection, and every lookup below is an LDS read instead of a chain of dependent
   // global ones. The lookups see the tables as they were before this call, as the global reads
@@ -1393,7 +1417,7 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   // from unhit slots, and no lookup reads an entry another thread writes. Updates go to memory.
   const bool cached = n_blocks <= kResCacheBlocks;
   constexpr int kTb = kResCacheBlocks / kResThreads, kTs = kMaxSlots / kResThreads;
-  int32_t tb[kTb], ts[kTs];
+  int32_t tb[kTb], ts[kTs], to[kTs];
   if (cached) {
 #pragma unroll
     for (int u = 0; u < kTb; ++u) {
@@ -1403,8 +1427,13 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
 #pragma unroll
     for (int u = 0; u < kTs; ++u) {
       const int i = threadIdx.x + u * kResThreads;
-      ts[u] = i < k ? sblock_h[i] : -1;
+      ts[u] = i < n_slots ? sblock_h[i] : -1;
     }
+  }
+#pragma unroll
+  for (int u = 0; u < kTs; ++u) {
+    const int i = threadIdx.x + u * kResThreads;
+    to[u] = i < n_slots ? (order_h != nullptr ? order_h[i] : i) : -1;
   }
   if constexpr (SEL) {
     // The head's top k, ascending, into LDS for the residency pass and to `ids` for the decode.
@@ -1424,11 +1453,15 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
     }
     __syncthreads();
   }
-  const int n_slots = k;
-  const int per = (k + kResThreads - 1) / kResThreads;  // <= kResPer
+  const int per = (k + kResThreads - 1) / kResThreads;         // items per thread, <= kResPer
+  const int ps = (n_slots + kResThreads - 1) / kResThreads;    // slots (and order positions) per thread, <= kResPer
   const int i0 = threadIdx.x * per;
+  const int s0 = threadIdx.x * ps;
   const int32_t* idx_h = idx + (int64_t)h * idx_stride;
-  for (int i = threadIdx.x; i < kMaxSlots / 32; i += kResThreads) hit[i] = 0u;
+  for (int i = threadIdx.x; i < kMaxSlots / 32; i += kResThreads) {
+    hit[i] = 0u;
+    used[i] = 0u;
+  }
   if (cached) {
 #pragma unroll
     for (int u = 0; u < kTb; ++u) {
@@ -1438,10 +1471,36 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
 #pragma unroll
     for (int u = 0; u < kTs; ++u) {
       const int i = threadIdx.x + u * kResThreads;
-      if (i < k) s_sblock[i] = ts[u];
+      if (i < n_slots) s_sblock[i] = ts[u];
     }
-    __syncthreads();
   }
+#pragma unroll
+  for (int u = 0; u < kTs; ++u) {
+    const int i = threadIdx.x + u * kResThreads;
+    if (i < n_slots) s_order[i] = to[u];
+  }
+  __syncthreads();
+  // The order must name every slot once. Count first occurrences of in-range entries; anything
+  // short of n_slots (an entry out of range or repeated) and the head's order is ascending slots.
+  uint32_t firsts = 0u;
+#pragma unroll
+  for (int u = 0; u < kTs; ++u) {
+    const int i = threadIdx.x + u * kResThreads;
+    const int sl = i < n_slots ? s_order[i] : -1;
+    if (sl >= 0 && sl < n_slots && !(atomicOr(&used[sl >> 5], 1u << (sl & 31)) & (1u << (sl & 31)))) ++firsts;
+  }
+  uint32_t n_firsts;
+  res_block_scan(firsts, scan_a, &n_firsts);
+  const bool order_ok = (int)n_firsts == n_slots;
+  if (!order_ok) {
+    // Not a permutation: ascending slot order. Every thread reads its positions from here on.
+#pragma unroll
+    for (int u = 0; u < kTs; ++u) {
+      const int i = threadIdx.x + u * kResThreads;
+      if (i < n_slots) s_order[i] = i;
+    }
+  }
+  for (int i = threadIdx.x; i < kMaxSlots / 32; i += kResThreads) used[i] = 0u;
   // This thread's items [i0, i0 + per): their blocks and current slots.
   int32_t blk[kResPer], cur[kResPer];
 #pragma unroll
@@ -1454,28 +1513,31 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   }
   // A hit needs both tables to agree (block_slot[b] = s and slot_block[s] = b): tables a caller
   // left inconsistent (or filled with zeros instead of -1) can then cost misses, never a read of
-  // a slot that holds another block.
+  // a slot that holds another block. Distinct blocks therefore hit distinct slots.
 #pragma unroll
   for (int u = 0; u < kResPer; ++u)
     if (cur[u] >= 0 && (cached ? s_sblock[cur[u]] : sblock_h[cur[u]]) != blk[u]) cur[u] = -1;
-  __syncthreads();
+  __syncthreads();  // the order is settled and `used` cleared
 #pragma unroll
   for (int u = 0; u < kResPer; ++u)
     if (cur[u] >= 0) atomicOr(&hit[cur[u] >> 5], 1u << (cur[u] & 31));
   __syncthreads();
-  // Victims: the unhit slots, ascending. Thread t owns slots [t*per, t*per + per).
+  // Victim candidates: the unhit slots in least-recently-used order. Thread t owns order positions
+  // [t*ps, t*ps + ps).
   uint32_t free_mask = 0u;
+  int32_t oslot[kResPer];
 #pragma unroll
   for (int u = 0; u < kResPer; ++u) {
-    const int sl = i0 + u;
-    const bool in = u < per && sl < n_slots && !((hit[sl >> 5] >> (sl & 31)) & 1u);
+    const int p = s0 + u;
+    oslot[u] = (u < ps && p < n_slots) ? s_order[p] : -1;
+    const bool in = oslot[u] >= 0 && !((hit[oslot[u] >> 5] >> (oslot[u] & 31)) & 1u);
     free_mask |= (in ? 1u : 0u) << u;
   }
   uint32_t n_free;
   uint32_t vpos = res_block_scan(__popc(free_mask), scan_a, &n_free);
 #pragma unroll
   for (int u = 0; u < kResPer; ++u) {
-    if ((free_mask >> u) & 1u) victims[vpos++] = i0 + u;
+    if ((free_mask >> u) & 1u) victims[vpos++] = oslot[u];
   }
   // Misses, ordinal in ascending item (= block) order.
   uint32_t miss_mask = 0u;
@@ -1491,7 +1553,7 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
     if (cur[u] >= 0) {
       loc_h[i] = cur[u];
     } else if (cur[u] == -2 || mpos >= n_free) {
-      loc_h[i] = -1;  // outside the pool (or no slot left, which a consistent table rules out)
+      loc_h[i] = -1;  // outside the pool (or no slot left, which n_slots >= k rules out)
     } else {
       const int v = victims[mpos++];
       const int32_t old = cached ? s_sblock[v] : sblock_h[v];
@@ -1502,6 +1564,30 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
       bslot_h[blk[u]] = v;
       loc_h[i] = kLocMiss | v;
     }
+  }
+  if (order_h == nullptr) return;  // no order to keep (the caller's slots all turn over each step)
+  // The new order: the slots this step did not use, in their old order, then the used ones (hits
+  // and the victims that were taken), ascending.
+  const uint32_t n_taken = min(n_miss, n_free);
+  for (int j = threadIdx.x; j < (int)n_taken; j += kResThreads) atomicOr(&used[victims[j] >> 5], 1u << (victims[j] & 31));
+  for (int i = threadIdx.x; i < kMaxSlots / 32; i += kResThreads) atomicOr(&used[i], hit[i]);
+  __syncthreads();
+  uint32_t keep_mask = 0u, use_mask = 0u;
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u) {
+    const bool kept = oslot[u] >= 0 && !((used[oslot[u] >> 5] >> (oslot[u] & 31)) & 1u);
+    keep_mask |= (kept ? 1u : 0u) << u;
+    const int sl = s0 + u;
+    const bool usd = u < ps && sl < n_slots && ((used[sl >> 5] >> (sl & 31)) & 1u);
+    use_mask |= (usd ? 1u : 0u) << u;
+  }
+  uint32_t n_kept, n_used;
+  uint32_t kpos = res_block_scan(__popc(keep_mask), scan_a, &n_kept);
+  uint32_t upos = res_block_scan(__popc(use_mask), scan_b, &n_used) + n_kept;
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u) {
+    if ((keep_mask >> u) & 1u) order_h[kpos++] = oslot[u];
+    if ((use_mask >> u) & 1u) order_h[upos++] = s0 + u;
   }
 }
 
@@ -1556,13 +1642,6 @@ extern "C" size_t lkv_sparse_decode_workspace_bytes(const lkv_decode_desc* d) {
   return lkv_align_up((size_t)d->n_kv * S * G * 2 * 4, 256) + lkv_align_up((size_t)d->n_kv * S * G * d->head_dim * 4, 256);
 }
 
-// Residency tables of a hybrid call (see residency_kernel).
-struct ResidencyArgs {
-  int32_t* block_slot;
-  int64_t block_slot_stride;
-  int32_t* slot_block;
-  int64_t slot_block_stride;
-};
 
 // A fused selection: the bound kernel scores every candidate into `bounds`, then the decode launch
 // picks each head's top k from them itself.
@@ -1591,7 +1670,7 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
                               const lkv_kv_source* sel, const int32_t* idx, int64_t idx_stride,
                               const lkv_kv_source* sink, const lkv_kv_source* cur, const lkv_kv_source* rem,
                               void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes,
-                              const lkv_kv_source* slots, int32_t* loc, int64_t loc_stride, const ResidencyArgs* res,
+                              const lkv_kv_source* slots, int32_t* loc, int64_t loc_stride, const lkv_residency* res,
                               const FusedSelect* fsel = nullptr) {
   LKV_CHECK_ARG(desc != nullptr && q != nullptr && out != nullptr && lse != nullptr, "NULL argument");
   const lkv_decode_desc& d = *desc;
@@ -1690,11 +1769,18 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
   a.loc = loc;
   a.loc_stride = loc_stride;
   if (slots) a.slots = to_src(slots);
-  // Inside the decode launch only while each thread holds at most kFuseKeysPerThread of the head's
-  // candidates; beyond, the selection takes a launch of its own.
-  const bool select_in_decode = fsel != nullptr && fsel->in_decode && fsel->n_cand <= kFuseKeysPerThread * p.nt;
+  // Inside the decode launch only where that launch takes the instance the unfused call takes, so
+  // that both fold the same items in the same order, and while each of its threads holds at most
+  // kFuseKeysPerThread of the head's candidates; otherwise the selection takes a launch of its own.
+  bool select_in_decode = false;
+  if (fsel != nullptr && fsel->in_decode) {
+    const Inst fused = pick_instance(a, d.head_dim, mt, G, true);
+    select_in_decode = fused == pick_instance(a, d.head_dim, mt, G, false) && fsel->n_cand <= kFuseKeysPerThread * inst_threads(fused);
+  }
   if (fsel != nullptr) {
-    LKV_CHECK_ARG(attend_sel && !has_rem, "a fused selection attends a selection, with no remainder");
+    // A remainder excludes the selected ids, so they must exist before the decode launch: chosen by
+    // their own launch or by the residency launch, not inside the decode launch.
+    LKV_CHECK_ARG(attend_sel && (!has_rem || !fsel->in_decode), "a selection inside the decode launch takes no remainder");
     LKV_CHECK_ARG(res == nullptr || !fsel->in_decode, "a hybrid call selects before its residency launch");
     LKV_CHECK_ARG(!fsel->in_residency || (res != nullptr && fsel->n_cand <= kSelCap && d.k <= kMaxSlots),
                   "a selection inside the residency launch takes at most %d candidates", kSelCap);
@@ -1732,14 +1818,14 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
     if (rc != LKV_OK) return rc;
   }
   if (res) {  // every argument is checked: update the residency tables, then attend
+    const ResTables t{res->block_slot, res->block_slot_stride, sel->n_blocks, res->slot_block, res->slot_block_stride,
+                      res->order, res->order_stride, (int)slots->n_blocks};
     if (fsel != nullptr && fsel->in_residency) {
       const ResSelect rs{fsel->bounds, fsel->stride, fsel->n_cand, fsel->cand_offset, fsel->aligned ? 1 : 0, fsel->ids, fsel->ids_stride};
-      hipLaunchKernelGGL(residency_kernel<true>, dim3(d.n_kv), dim3(kResThreads), 0, s, fsel->ids, fsel->ids_stride, d.k,
-                         res->block_slot, res->block_slot_stride, sel->n_blocks, res->slot_block, res->slot_block_stride, loc,
+      hipLaunchKernelGGL(residency_kernel<true>, dim3(d.n_kv), dim3(kResThreads), 0, s, fsel->ids, fsel->ids_stride, d.k, t, loc,
                          loc_stride, rs);
     } else {
-      hipLaunchKernelGGL(residency_kernel<false>, dim3(d.n_kv), dim3(kResThreads), 0, s, a.idx, a.idx_stride, d.k,
-                         res->block_slot, res->block_slot_stride, sel->n_blocks, res->slot_block, res->slot_block_stride, loc,
+      hipLaunchKernelGGL(residency_kernel<false>, dim3(d.n_kv), dim3(kResThreads), 0, s, a.idx, a.idx_stride, d.k, t, loc,
                          loc_stride, ResSelect{});
     }
     LKV_CHECK_LAUNCH("residency");
@@ -1769,43 +1855,43 @@ extern "C" size_t lkv_hybrid_decode_workspace_bytes(const lkv_decode_desc* d) {
   return base + lkv_align_up((size_t)d->n_kv * (size_t)(d->k > 0 ? d->k : 0) * 4, 256);
 }
 
-// What a hybrid call adds to a decode call: a host pool, an HBM slot per selected block, and the
-// tables of which block each slot holds.
-static int check_hybrid(const lkv_decode_desc& d, const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* block_slot,
-                        int64_t block_slot_stride, const int32_t* slot_block, int64_t slot_block_stride) {
-  LKV_CHECK_ARG(host != nullptr && slots != nullptr, "NULL argument");
+// What a hybrid call adds to a decode call: a host pool, n_slots >= k HBM slots per head, and the
+// tables of which block each slot holds (and, with spare slots, their use order).
+static int check_hybrid(const lkv_decode_desc& d, const lkv_kv_source* host, const lkv_kv_source* slots, const lkv_residency* res) {
+  LKV_CHECK_ARG(host != nullptr && slots != nullptr && res != nullptr, "NULL argument");
   LKV_CHECK_ARG(d.attend_selected && d.k > 0, "hybrid decode attends a selection: k > 0 and attend_selected");
-  LKV_CHECK_ARG(d.rem_last == d.rem_first, "hybrid decode has no remainder");
-  LKV_CHECK_ARG(d.k <= kMaxSlots, "k=%d exceeds the hybrid slot limit %d", d.k, kMaxSlots);
   LKV_CHECK_ARG(d.n_kv > 0, "bad n_kv");
   const int model = host->dtype == LKV_INT8_RECORD ? host->deq_dtype : host->dtype;
   LKV_CHECK_ARG(host->dtype == LKV_INT8_RECORD || (lkv_is_model_dtype(host->dtype) && host->v != nullptr),
                 "the hybrid host pool holds model-dtype pairs or int8 records");
   LKV_CHECK_ARG(slots->dtype == model && lkv_is_model_dtype(model) && slots->k != nullptr && slots->v != nullptr,
                 "slots must hold the model dtype (the host pool's, or its records' dequantised dtype)");
-  LKV_CHECK_ARG(slots->n_blocks == d.k, "the slot pool holds k=%d slots per head, got %lld", d.k, (long long)slots->n_blocks);
-  LKV_CHECK_ARG(block_slot != nullptr && slot_block != nullptr, "residency tables missing");
-  LKV_CHECK_ARG(block_slot_stride >= host->n_blocks && slot_block_stride >= d.k, "residency table strides too small");
+  const int64_t n_slots = slots->n_blocks;
+  LKV_CHECK_ARG(n_slots >= d.k, "%lld slots per head cannot hold a selection of k=%d blocks", (long long)n_slots, d.k);
+  LKV_CHECK_ARG(n_slots <= kMaxSlots, "%lld slots per head exceed the hybrid slot limit %d", (long long)n_slots, kMaxSlots);
+  LKV_CHECK_ARG(res->block_slot != nullptr && res->slot_block != nullptr, "residency tables missing");
+  LKV_CHECK_ARG(res->block_slot_stride >= host->n_blocks && res->slot_block_stride >= n_slots, "residency table strides too small");
+  LKV_CHECK_ARG(res->order != nullptr || n_slots == d.k, "%lld slots for k=%d need the slots' use order", (long long)n_slots, d.k);
+  LKV_CHECK_ARG(res->order == nullptr || res->order_stride >= n_slots, "slot order stride too small");
   return LKV_OK;
 }
 
 extern "C" int lkv_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype,
                                  const lkv_kv_source* host, const lkv_kv_source* slots, const int32_t* idx,
-                                 int64_t idx_stride, int32_t* block_slot, int64_t block_slot_stride, int32_t* slot_block,
-                                 int64_t slot_block_stride, const lkv_kv_source* sink, const lkv_kv_source* cur,
-                                 void* out, int out_dtype, float* lse, void* ws, size_t ws_bytes) {
+                                 int64_t idx_stride, const lkv_residency* res, const lkv_kv_source* sink,
+                                 const lkv_kv_source* cur, const lkv_kv_source* rem, void* out, int out_dtype, float* lse,
+                                 void* ws, size_t ws_bytes) {
   LKV_CHECK_ARG(desc != nullptr && host != nullptr && slots != nullptr && idx != nullptr, "NULL argument");
   const lkv_decode_desc& d = *desc;
-  const int rc = check_hybrid(d, host, slots, block_slot, block_slot_stride, slot_block, slot_block_stride);
+  const int rc = check_hybrid(d, host, slots, res);
   if (rc != LKV_OK) return rc;
   LKV_CHECK_ARG(idx_stride >= d.k, "bad idx_stride");
   const size_t need = lkv_hybrid_decode_workspace_bytes(desc);
   LKV_CHECK_ARG(ws != nullptr && ws_bytes >= need, "workspace of %zu bytes needed, got %zu", need, ws_bytes);
   const size_t dec_bytes = lkv_sparse_decode_workspace_bytes(desc);
   int32_t* loc = (int32_t*)((char*)ws + dec_bytes);  // dec_bytes is a multiple of 256
-  const ResidencyArgs res{block_slot, block_slot_stride, slot_block, slot_block_stride};
-  return sparse_decode_impl(stream, desc, q, q_dtype, host, idx, idx_stride, sink, cur, nullptr, out, out_dtype, lse, ws,
-                            dec_bytes, slots, loc, (int64_t)d.k, &res);
+  return sparse_decode_impl(stream, desc, q, q_dtype, host, idx, idx_stride, sink, cur, rem, out, out_dtype, lse, ws,
+                            dec_bytes, slots, loc, (int64_t)d.k, res);
 }
 
 // ---- allocation-free variant of lkv_sparse_decode ------------------------------------------------
@@ -1939,10 +2025,10 @@ extern "C" size_t lkv_select_hybrid_decode_workspace_bytes(const lkv_decode_desc
 
 extern "C" int lkv_select_hybrid_decode(uintptr_t stream, const lkv_decode_desc* desc, const void* q, int q_dtype, const void* kmin,
                                         const void* kmax, int meta_dtype, int64_t meta_head_stride, int cand_offset, int n_cand,
-                                        int rank_mode, const lkv_kv_source* host, const lkv_kv_source* slots, int32_t* block_slot,
-                                        int64_t block_slot_stride, int32_t* slot_block, int64_t slot_block_stride,
-                                        const lkv_kv_source* sink, const lkv_kv_source* cur, void* out, int out_dtype, float* lse,
-                                        int32_t* out_idx, int64_t idx_stride, void* ws, size_t ws_bytes) {
+                                        int rank_mode, const lkv_kv_source* host, const lkv_kv_source* slots,
+                                        const lkv_residency* res, const lkv_kv_source* sink, const lkv_kv_source* cur,
+                                        const lkv_kv_source* rem, void* out, int out_dtype, float* lse, int32_t* out_idx,
+                                        int64_t idx_stride, void* ws, size_t ws_bytes) {
   LKV_CHECK_ARG(desc != nullptr && q != nullptr && kmin != nullptr && kmax != nullptr, "NULL argument");
   const lkv_decode_desc& d = *desc;
   LKV_CHECK_ARG(d.head_dim == 64 || d.head_dim == 128, "head_dim %d unsupported (64 or 128)", d.head_dim);
@@ -1958,7 +2044,7 @@ extern "C" int lkv_select_hybrid_decode(uintptr_t stream, const lkv_decode_desc*
   LKV_CHECK_ARG(d.k > 0 && d.k <= n_cand && d.attend_selected, "selected k=%d must be in 1..n_cand=%d, attended", d.k, n_cand);
   LKV_CHECK_ARG(meta_head_stride >= (int64_t)(cand_offset + n_cand) * d.head_dim, "metadata head stride too small");
   LKV_CHECK_ARG(out_idx == nullptr || idx_stride >= d.k, "idx_stride < k");
-  const int rc = check_hybrid(d, host, slots, block_slot, block_slot_stride, slot_block, slot_block_stride);
+  const int rc = check_hybrid(d, host, slots, res);
   if (rc != LKV_OK) return rc;
   const size_t dec = lkv_sparse_decode_workspace_bytes(desc);
   const size_t hyb = lkv_hybrid_decode_workspace_bytes(desc);
@@ -1986,7 +2072,6 @@ extern "C" int lkv_select_hybrid_decode(uintptr_t stream, const lkv_decode_desc*
     fs.ids = (int32_t*)((char*)fs.bounds + lkv_align_up((size_t)d.n_kv * (size_t)fs.stride * 4, 256));
     fs.ids_stride = d.k;
   }
-  const ResidencyArgs res{block_slot, block_slot_stride, slot_block, slot_block_stride};
-  return sparse_decode_impl(stream, desc, q, q_dtype, host, nullptr, 0, sink, cur, nullptr, out, out_dtype, lse, ws, dec, slots, loc,
-                            (int64_t)d.k, &res, &fs);
+  return sparse_decode_impl(stream, desc, q, q_dtype, host, nullptr, 0, sink, cur, rem, out, out_dtype, lse, ws, dec, slots, loc,
+                            (int64_t)d.k, res, &fs);
 }

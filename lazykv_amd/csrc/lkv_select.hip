@@ -785,8 +785,10 @@ template <int D, int MT, int G>
 int launch_bound(hipStream_t stream, const void* q, int q_dtype, const void* kmin, const void* kmax, int64_t mhs, int n_kv,
                  int cand_offset, int n_cand, int rank_mode, float* bounds, int64_t bstride) {
   using T = typename lkv::Elem<MT>::T;
-  // A model-dtype query, and 16-byte aligned rows (the strides are multiples of 128 bytes): the matrix cores.
-  if (q_dtype == MT && (((uintptr_t)q | (uintptr_t)kmin | (uintptr_t)kmax) & 15u) == 0) {
+  // A model-dtype query and 16-byte aligned metadata rows: the matrix cores. A row starts at
+  // h * mhs + b * D elements; D is 64 or 128, so the rows are aligned when the bases are and the
+  // head stride is a multiple of 8 elements. Any other layout takes the vector kernel.
+  if (q_dtype == MT && (((uintptr_t)q | (uintptr_t)kmin | (uintptr_t)kmax) & 15u) == 0 && (mhs & 7) == 0) {
     const int splits_mf = (n_cand + kBoundMfBlocks - 1) / kBoundMfBlocks;
     hipLaunchKernelGGL((bound_kernel_mf<D, MT, G>), dim3(splits_mf * n_kv), dim3(kBoundMfThreads), 0, stream, (const uint16_t*)q,
                        (const uint16_t*)kmin, (const uint16_t*)kmax, mhs, n_kv, cand_offset, n_cand, rank_mode, bounds, bstride);

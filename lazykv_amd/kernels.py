@@ -258,7 +258,8 @@ class PreparedSelectDecode:
     """`lkv_select_decode` with its arguments converted once: the Quest bound of candidates
     cand_offset .. cand_offset + n_cand - 1 from metadata `[1, h, cap, d]`, the top k per head, and
     the block-sparse decode over sink + selected (from `sel`) + current. `desc.fill` /
-    `desc.cur_block` and `n_cand` (`set_candidates`, within `max_cand`) may change between calls."""
+    `desc.cur_block` and `n_cand` (`set_candidates`, up to the count the workspace was sized for) may
+    change between calls."""
 
     def __init__(self, q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, block_size: int,
                  scale: float, sel: Source, sink: Source | None, sink_block: int, cur: Source | None, cur_block: int, fill: int,
@@ -288,12 +289,16 @@ class PreparedSelectDecode:
         self._tail = (rank_mode, refs[0], refs[1], refs[2], out.data_ptr(), _lib.dtype_code(out.dtype), lse.data_ptr(),
                       out_idx.data_ptr() if out_idx is not None else None, k, ws_ptr, ws_n)
         self.n_cand = n_cand
-        self._cap = cap - cand_offset
+        self._sized = sizing
+        self._cap = min(cap - cand_offset, sizing)
         self.device = q.device
 
     def set_candidates(self, n_cand: int) -> None:
+        """A new candidate count, up to the one the workspace was sized for (the constructor's
+        n_cand, or max_cand). The count decides where the top K is chosen and which kernel instance
+        runs, so a HIP graph captured before the change must be captured again after it."""
         if not self.desc.k <= n_cand <= self._cap:
-            raise ValueError(f"{n_cand} candidates for k={self.desc.k}")
+            raise ValueError(f"{n_cand} candidates for k={self.desc.k}: at most {self._cap} (the workspace was sized for {self._sized})")
         self.n_cand = n_cand
 
     def __call__(self) -> None:
@@ -322,18 +327,61 @@ def select_decode(q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: in
 
 @dataclass
 class Residency:
-    """HBM slots of one layer (`slots` [k, h, 2, bs, d]) and the tables that say what they hold:
-    block_slot [h, cap] (slot or -1), slot_block [h, k] (block or -1), both int32 on the GPU."""
+    """HBM slots of one layer (`slots` [n_slots, h, 2, bs, d]) and the tables that say what they hold:
+    block_slot [h, cap] (slot or -1), slot_block [h, n_slots] (block or -1), and `order` [h, n_slots]:
+    each head's slots from least to most recently used, ties to the lower slot. All int32 on the GPU.
+    With n_slots == k the order decides only which unhit slot a missed block lands in (every unhit
+    slot is evicted), and the library accepts None there; `allocate` always keeps it, so the tables
+    follow the reference's least-recently-used rule slot for slot."""
 
     slots: torch.Tensor
     block_slot: torch.Tensor
     slot_block: torch.Tensor
+    order: torch.Tensor | None = None
 
     @classmethod
-    def allocate(cls, k: int, h: int, cap_blocks: int, block_size: int, head_dim: int, dtype: torch.dtype, device: torch.device) -> Residency:
-        return cls(torch.zeros((k, h, 2, block_size, head_dim), dtype=dtype, device=device),
+    def allocate(cls, k: int, h: int, cap_blocks: int, block_size: int, head_dim: int, dtype: torch.dtype, device: torch.device,
+                 n_slots: int | None = None) -> Residency:
+        n = k if n_slots is None else n_slots
+        if n < k:
+            raise ValueError(f"{n} slots cannot hold a selection of {k} blocks")
+        order = torch.arange(n, dtype=torch.int32, device=device).repeat(h, 1)
+        return cls(torch.zeros((n, h, 2, block_size, head_dim), dtype=dtype, device=device),
                    torch.full((h, cap_blocks), -1, dtype=torch.int32, device=device),
-                   torch.full((h, k), -1, dtype=torch.int32, device=device))
+                   torch.full((h, n), -1, dtype=torch.int32, device=device), order)
+
+    @property
+    def n_slots(self) -> int:
+        return self.slots.shape[0]
+
+    def seed(self, first: int, n: int) -> None:
+        """Record that slots 0..n-1 of every head hold blocks first..first+n-1 (the caller has written
+        them), with the empty slots least recently used: the reference's seeded residency
+        (lazykv/tiered.py:274-287). Device-side fills only."""
+        dev = self.slot_block.device
+        blocks = torch.arange(first, first + n, dtype=torch.int32, device=dev)
+        self.slot_block[:, :n] = blocks
+        self.block_slot[:, first : first + n] = torch.arange(n, dtype=torch.int32, device=dev)
+        if self.order is not None:
+            used = torch.cat([torch.arange(n, self.n_slots, device=dev), torch.arange(0, n, device=dev)]).to(torch.int32)
+            self.order.copy_(used.expand_as(self.order))
+
+    def tables(self) -> _lib.ResidencyTables:
+        order = self.order
+        return _lib.ResidencyTables(self.block_slot.data_ptr(), self.block_slot.stride(0), self.slot_block.data_ptr(), self.slot_block.stride(0),
+                                    order.data_ptr() if order is not None else None, order.stride(0) if order is not None else 0)
+
+    def check(self, n_kv: int, n_blocks: int, k: int) -> None:
+        """Shapes the residency launch relies on: tables with contiguous rows covering the pool's
+        blocks and the slots, and n_slots >= k."""
+        n = self.n_slots
+        for t, want in ((self.block_slot, n_blocks), (self.slot_block, n)) + (((self.order, n),) if self.order is not None else ()):
+            if t.dtype != torch.int32 or t.ndim != 2 or t.shape[0] != n_kv or t.shape[1] < want or t.stride(1) != 1:
+                raise ValueError(f"residency table must be int32 [{n_kv}, >= {want}] with contiguous rows, got {tuple(t.shape)} {t.dtype}")
+        if n < k:
+            raise ValueError(f"the slot pool holds {n} slots per head, fewer than k={k}")
+        if n > k and self.order is None:
+            raise ValueError(f"{n} slots for k={k} need the slots' use order")
 
 
 def hybrid_decode(
@@ -350,15 +398,18 @@ def hybrid_decode(
     cur: Source | None = None,
     cur_block: int = -1,
     fill: int = 0,
+    rem: Source | None = None,
+    rem_range: tuple[int, int] = (0, 0),
     out: torch.Tensor | None = None,
     out_dtype: torch.dtype | None = None,
     lse: torch.Tensor | None = None,
     ws: Workspace | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """lkv_hybrid_decode: `sparse_decode` over `host` with the selected pairs in `res`'s slots read
-    from HBM, the others read in place and admitted. Updates `res`'s tables."""
+    from HBM, the others read in place and admitted; with `rem`, also every block of `rem_range` the
+    selection does not name (the exact tier's remainder). Updates `res`'s tables."""
     p = PreparedHybridDecode(q, n_kv=n_kv, block_size=block_size, scale=scale, host=host, res=res, idx=idx, sink=sink, sink_block=sink_block,
-                             cur=cur, cur_block=cur_block, fill=fill, out=out, out_dtype=out_dtype, lse=lse, ws=ws)
+                             cur=cur, cur_block=cur_block, fill=fill, rem=rem, rem_range=rem_range, out=out, out_dtype=out_dtype, lse=lse, ws=ws)
     p()
     return p.out, p.lse
 
@@ -367,33 +418,31 @@ class PreparedHybridDecode:
     """`hybrid_decode` with its arguments converted once; `desc.fill` / `desc.cur_block` may change between calls."""
 
     def __init__(self, q: torch.Tensor, *, n_kv: int, block_size: int, scale: float, host: Source, res: Residency, idx: torch.Tensor, sink: Source | None,
-                 sink_block: int, cur: Source | None, cur_block: int, fill: int, out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-                 lse: torch.Tensor | None = None, ws: Workspace | None = None) -> None:
+                 sink_block: int, cur: Source | None, cur_block: int, fill: int, rem: Source | None = None, rem_range: tuple[int, int] = (0, 0),
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None, lse: torch.Tensor | None = None, ws: Workspace | None = None) -> None:
         _lib.require_cuda(q, idx, res.slots, res.block_slot, res.slot_block)
         qq = q.reshape(-1, q.shape[-1]).contiguous()
         n_q, d = qq.shape
         if idx.dtype != torch.int32 or idx.ndim != 2 or idx.shape[0] != n_kv or not idx.is_contiguous():
             raise ValueError(f"idx must be contiguous int32 [{n_kv}, k], got {tuple(idx.shape)} {idx.dtype}")
         k = idx.shape[1]
-        for t, shape in ((res.block_slot, (n_kv, host.n_blocks)), (res.slot_block, (n_kv, k))):
-            if t.dtype != torch.int32 or t.ndim != 2 or tuple(t.shape[:1]) != shape[:1] or t.shape[1] < shape[1] or t.stride(1) != 1:
-                raise ValueError(f"residency table must be int32 [{shape[0]}, >= {shape[1]}] with contiguous rows, got {tuple(t.shape)} {t.dtype}")
-        if res.slots.shape[0] != k:
-            raise ValueError(f"the slot pool must hold k={k} slots, got {res.slots.shape[0]}")
+        res.check(n_kv, host.n_blocks, k)
         out_dtype = out_dtype or (out.dtype if out is not None else qq.dtype)
         self.out = out if out is not None else torch.empty((n_q, d), dtype=out_dtype, device=q.device)
         self.lse = lse if lse is not None else torch.empty((n_q,), dtype=torch.float32, device=q.device)
-        self.desc = _lib.DecodeDesc(n_q, n_kv, d, block_size, float(scale), k, 1, sink_block, cur_block, fill, 0, 0)
+        r0, r1 = rem_range if rem is not None else (0, 0)
+        self.desc = _lib.DecodeDesc(n_q, n_kv, d, block_size, float(scale), k, 1, sink_block, cur_block, fill, r0, r1)
         ws = ws or default_workspace(q.device)
         ws_ptr, ws_n = ws.get(_lib.lib().lkv_hybrid_decode_workspace_bytes(ctypes.byref(self.desc)))
         slot_src = pool_source(res.slots)
-        self._c = [s.c() if s is not None else None for s in (host, slot_src, sink, cur)]
+        self._c = [s.c() if s is not None else None for s in (host, slot_src, sink, cur, rem)]
+        self._tables = res.tables()
         refs = [ctypes.byref(c) if c is not None else None for c in self._c]
-        self._keep = (qq, idx, self.out, self.lse, ws.buf, host, res, sink, cur)
+        self._keep = (qq, idx, self.out, self.lse, ws.buf, host, res, sink, cur, rem)
         self._fn = _lib.lib().lkv_hybrid_decode
         self._args = (ctypes.byref(self.desc), qq.data_ptr(), _lib.dtype_code(qq.dtype), refs[0], refs[1], idx.data_ptr(), idx.stride(0),
-                      res.block_slot.data_ptr(), res.block_slot.stride(0), res.slot_block.data_ptr(), res.slot_block.stride(0), refs[2], refs[3],
-                      self.out.data_ptr(), _lib.dtype_code(self.out.dtype), self.lse.data_ptr(), ws_ptr, ws_n)
+                      ctypes.byref(self._tables), refs[2], refs[3], refs[4], self.out.data_ptr(), _lib.dtype_code(self.out.dtype),
+                      self.lse.data_ptr(), ws_ptr, ws_n)
         self.device = q.device
 
     def __call__(self) -> None:
@@ -406,14 +455,15 @@ class PreparedSelectHybridDecode:
     """`lkv_select_hybrid_decode` with its arguments converted once: the Quest bound of candidates
     cand_offset .. cand_offset + n_cand - 1 from metadata `[1, h, cap, d]`, the top k per head chosen
     by the launch that updates `res`'s tables, and the hybrid decode over sink + selected (hits from
-    `res`'s slots, misses from `host`) + current. Equals `PreparedBoundTopk` followed by
-    `PreparedHybridDecode`, bit for bit. `desc.fill` / `desc.cur_block` and `n_cand`
-    (`set_candidates`, within `max_cand`) may change between calls."""
+    `res`'s slots, misses from `host`) + current, plus, with `rem`, the exact tier's remainder.
+    Equals `PreparedBoundTopk` followed by `PreparedHybridDecode`, bit for bit. `desc.fill` /
+    `desc.cur_block` and `n_cand` (`set_candidates`, up to the count the workspace was sized for)
+    may change between calls."""
 
     def __init__(self, q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, block_size: int,
                  scale: float, host: Source, res: Residency, sink: Source | None, sink_block: int, cur: Source | None, cur_block: int, fill: int,
-                 out: torch.Tensor, lse: torch.Tensor, rank_mode: int = _lib.RANK_F32, out_idx: torch.Tensor | None = None,
-                 ws: Workspace | None = None, max_cand: int | None = None) -> None:
+                 out: torch.Tensor, lse: torch.Tensor, rem: Source | None = None, rem_range: tuple[int, int] = (0, 0), rank_mode: int = _lib.RANK_F32,
+                 out_idx: torch.Tensor | None = None, ws: Workspace | None = None, max_cand: int | None = None) -> None:
         _lib.require_cuda(q, kmin, kmax, out, lse, res.slots, res.block_slot, res.slot_block)
         n_kv, cap, d, hs = _meta_layout(kmin, kmax)
         qq = q.reshape(-1, d)
@@ -425,31 +475,33 @@ class PreparedSelectHybridDecode:
             raise ValueError("out must be contiguous [n_q, d] and lse contiguous float32 [n_q]")
         if out_idx is not None and (out_idx.dtype != torch.int32 or tuple(out_idx.shape) != (n_kv, k) or not out_idx.is_contiguous()):
             raise ValueError(f"out_idx must be contiguous int32 [{n_kv}, {k}]")
-        for t, shape in ((res.block_slot, (n_kv, host.n_blocks)), (res.slot_block, (n_kv, k))):
-            if t.dtype != torch.int32 or t.ndim != 2 or tuple(t.shape[:1]) != shape[:1] or t.shape[1] < shape[1] or t.stride(1) != 1:
-                raise ValueError(f"residency table must be int32 [{shape[0]}, >= {shape[1]}] with contiguous rows, got {tuple(t.shape)} {t.dtype}")
-        if res.slots.shape[0] != k:
-            raise ValueError(f"the slot pool must hold k={k} slots, got {res.slots.shape[0]}")
+        res.check(n_kv, host.n_blocks, k)
         self.desc = _select_desc(qq, n_kv, block_size, scale, k, sink_block, cur_block, fill)
+        if rem is not None:
+            self.desc.rem_first, self.desc.rem_last = rem_range
         ws = ws or default_workspace(q.device)
         sizing = max(n_cand, max_cand or 0)
         ws_ptr, ws_n = ws.get(_lib.lib().lkv_select_hybrid_decode_workspace_bytes(ctypes.byref(self.desc), sizing))
-        self._c = [s.c() if s is not None else None for s in (host, pool_source(res.slots), sink, cur)]
+        self._c = [s.c() if s is not None else None for s in (host, pool_source(res.slots), sink, cur, rem)]
+        self._tables = res.tables()
         refs = [ctypes.byref(c) if c is not None else None for c in self._c]
-        self._keep = (q, kmin, kmax, out, lse, out_idx, ws.buf, host, res, sink, cur)
+        self._keep = (q, kmin, kmax, out, lse, out_idx, ws.buf, host, res, sink, cur, rem)
         self._fn = _lib.lib().lkv_select_hybrid_decode
         self._head = (ctypes.byref(self.desc), qq.data_ptr(), _lib.dtype_code(qq.dtype), address(kmin[0] if kmin.ndim == 4 else kmin),
                       address(kmax[0] if kmax.ndim == 4 else kmax), _lib.dtype_code(kmin.dtype), hs, cand_offset)
-        self._tail = (rank_mode, refs[0], refs[1], res.block_slot.data_ptr(), res.block_slot.stride(0), res.slot_block.data_ptr(),
-                      res.slot_block.stride(0), refs[2], refs[3], out.data_ptr(), _lib.dtype_code(out.dtype), lse.data_ptr(),
-                      out_idx.data_ptr() if out_idx is not None else None, k, ws_ptr, ws_n)
+        self._tail = (rank_mode, refs[0], refs[1], ctypes.byref(self._tables), refs[2], refs[3], refs[4], out.data_ptr(), _lib.dtype_code(out.dtype),
+                      lse.data_ptr(), out_idx.data_ptr() if out_idx is not None else None, k, ws_ptr, ws_n)
         self.n_cand = n_cand
-        self._cap = cap - cand_offset
+        self._sized = sizing
+        self._cap = min(cap - cand_offset, sizing)
         self.device = q.device
 
     def set_candidates(self, n_cand: int) -> None:
+        """A new candidate count, up to the one the workspace was sized for (the constructor's
+        n_cand, or max_cand). A HIP graph captured before the change keeps the old count: capture
+        again after it."""
         if not self.desc.k <= n_cand <= self._cap:
-            raise ValueError(f"{n_cand} candidates for k={self.desc.k}")
+            raise ValueError(f"{n_cand} candidates for k={self.desc.k}: at most {self._cap} (the workspace was sized for {self._sized})")
         self.n_cand = n_cand
 
     def __call__(self) -> None:
@@ -460,18 +512,19 @@ class PreparedSelectHybridDecode:
 
 def select_hybrid_decode(q: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, k: int, *, cand_offset: int, n_cand: int, block_size: int,
                          scale: float, host: Source, res: Residency, sink: Source | None = None, sink_block: int = -1, cur: Source | None = None,
-                         cur_block: int = -1, fill: int = 0, rank_mode: int = _lib.RANK_F32, out: torch.Tensor | None = None,
-                         out_dtype: torch.dtype | None = None, lse: torch.Tensor | None = None, out_idx: torch.Tensor | None = None,
-                         ws: Workspace | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """Bound + top-k + hybrid decode of one layer (lkv_select_hybrid_decode). Returns (out [n_q, d], lse [n_q])."""
+                         cur_block: int = -1, fill: int = 0, rem: Source | None = None, rem_range: tuple[int, int] = (0, 0),
+                         rank_mode: int = _lib.RANK_F32, out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                         lse: torch.Tensor | None = None, out_idx: torch.Tensor | None = None, ws: Workspace | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Bound + top-k + hybrid decode of one layer (lkv_select_hybrid_decode), with the exact tier's
+    remainder when `rem` is given. Returns (out [n_q, d], lse [n_q])."""
     qq = q.reshape(-1, q.shape[-1]).contiguous()
     n_q, d = qq.shape
     out_dtype = out_dtype or (out.dtype if out is not None else qq.dtype)
     out = out if out is not None else torch.empty((n_q, d), dtype=out_dtype, device=q.device)
     lse = lse if lse is not None else torch.empty((n_q,), dtype=torch.float32, device=q.device)
     PreparedSelectHybridDecode(qq, kmin, kmax, k, cand_offset=cand_offset, n_cand=n_cand, block_size=block_size, scale=scale, host=host, res=res,
-                               sink=sink, sink_block=sink_block, cur=cur, cur_block=cur_block, fill=fill, out=out, lse=lse, rank_mode=rank_mode,
-                               out_idx=out_idx, ws=ws)()
+                               sink=sink, sink_block=sink_block, cur=cur, cur_block=cur_block, fill=fill, out=out, lse=lse, rem=rem, rem_range=rem_range,
+                               rank_mode=rank_mode, out_idx=out_idx, ws=ws)()
     return out, lse
 
 

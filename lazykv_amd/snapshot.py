@@ -174,14 +174,23 @@ def restore(
     model: Any = None,
     host_pools: list[torch.Tensor] | None = None,
     n_slots: int | None = None,
-    fetch: str = "zerocopy",
+    fetch: str = "gather",
+    stages: Any = None,
+    unbuffered: bool = False,
     rebuild: str = "store",
     **tier_kwargs: Any,
 ) -> tuple[TieredCache, torch.Tensor, RestoreStats]:
     """A TieredCache at the snapshot's position and the logits for its next token
-    (lazykv/snapshot.py:184-278). `tier_kwargs` (exact, rank_dtype) go to the tiers and the cache."""
+    (lazykv/snapshot.py:184-278), with the reference's arguments and defaults. `fetch`, `n_slots`
+    and `stages` mean what they mean to TieredCache. `unbuffered=True` reads from the disk rather
+    than the page cache, what a session resumed long after its save pays: the reference opens the
+    file unbuffered (Windows only); here the file's cached pages are written back and dropped
+    (fdatasync, then POSIX_FADV_DONTNEED) before the reads. `tier_kwargs` (exact, rank_dtype) go to
+    the tiers and the cache."""
     if rebuild not in ("store", "boundary"):
         raise ValueError(f"rebuild must be 'store' or 'boundary', got {rebuild!r}")
+    if unbuffered and not hasattr(os, "posix_fadvise"):
+        raise NotImplementedError("the unbuffered read needs posix_fadvise")
     header, base = read_header(path)
     dtype = _NAMED_DTYPES[header["dtype"]]
     h, d, bs, length = header["heads"], header["head_dim"], header["block_size"], header["length"]
@@ -200,6 +209,9 @@ def restore(
     full = FullGPUCache(num_layers, capacity_tokens)
     tiers: dict[int, TieredLayer] = {}
     fd = os.open(path, os.O_RDONLY)
+    if unbuffered:
+        os.fdatasync(fd)  # dirty pages cannot be dropped
+        os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
 
     def section(name: str, out: torch.Tensor) -> torch.Tensor:
         """Read section `name` into the contiguous CPU tensor `out` (pinned pools included)."""
@@ -248,7 +260,8 @@ def restore(
     finally:
         os.close(fd)
     g0 = time.perf_counter()
-    cache = TieredCache(full, k_blocks, bs, capacity_tokens, model=model, dense_layers=header["dense_layers"], n_slots=n_slots, fetch=fetch, tiers=tiers, **tier_kwargs)
+    cache = TieredCache(full, k_blocks, bs, capacity_tokens, model=model, dense_layers=header["dense_layers"], n_slots=n_slots, fetch=fetch, stages=stages,
+                        tiers=tiers, **tier_kwargs)
     torch.cuda.synchronize()
     stats.rebuild_s += time.perf_counter() - g0
     return cache, logits, stats

@@ -136,6 +136,7 @@ def tiered_prefill(
     if chunk_size <= 0:
         raise ValueError(f"chunk_size must be positive, got {chunk_size}")
     tier_kw = {key: value for key, value in cache_kwargs.items() if key in _TIER_KW}
+    tier_kw.setdefault("fetch", "runs")  # the layers are read the way the cache will read them: its default
     torch.cuda.synchronize(device)
     start = time.perf_counter()
 

@@ -20,9 +20,12 @@ How each function is pinned (each check lives in `tests/test_oracle.py`):
 * `top_blocks`: brute-force sort; tie order (lower block id first) is the rule of lkv_bound_topk.
 * `block_minmax`, `current_block_mask`, `blocks_for_budget`: closed forms and the reference's
   own known answers (`tests/test_selection.py:38-44,98`).
-* `residency_step`: invariants that fix it (after a step the resident set is exactly the chosen
-  set, hits keep their slots, victims are exactly the unhit slots) and a least-recently-used
-  simulation in the reference's own terms (lazykv/tiered.py:389-418), on random step sequences.
+* `residency_state` / `residency_step` / `slot_order`: invariants that fix them (every chosen
+  block is resident after a step, hits keep their slots, the victims are the least recently used
+  unhit slots, and with as many slots as chosen blocks exactly the unhit ones), and a separate
+  least-recently-used simulation written over plain lists in the reference's own terms
+  (lazykv/tiered.py:274-287,389-418,450-452), on random step sequences with and without spare
+  slots and with a seeded start.
 * `attend` / `partial_attention` / `merge_lse`: float64 brute force over explicit token lists,
   the reference's merge known answer (`tests/test_exact.py:72-84`), the empty-partial rule
   (`tests/test_exact.py:52-69`) and the two-halves reconstruction (`tests/test_exact.py:32-49`).
@@ -334,36 +337,56 @@ def partial_attention(keys: np.ndarray, values: np.ndarray, query: np.ndarray, s
 LOC_MISS = 0x40000000
 
 
-def residency_step(block_slot: np.ndarray, slot_block: np.ndarray, chosen: np.ndarray) -> np.ndarray:
-    """One step of the hybrid tier's residency, per KV head, with as many slots as chosen blocks.
+def residency_state(h: int, n_slots: int, cap_blocks: int, first: int = 0, seed: int = 0) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """A hybrid tier's residency when its prompt closes (lazykv/tiered.py:165-168,274-287): slots
+    0..seed-1 of every head hold blocks first..first+seed-1 and were last used at -1; the other slots
+    are empty, last used at -2, so they are taken first. Returns block_slot [h, cap] (slot or -1),
+    slot_block [h, n_slots] (block or -1) and last_used [h, n_slots]. Slots are numbered from 0 here;
+    the reference numbers them 1..n_slots after the sink."""
+    block_slot = np.full((h, cap_blocks), -1, dtype=np.int64)
+    slot_block = np.full((h, n_slots), -1, dtype=np.int64)
+    last_used = np.full((h, n_slots), -2, dtype=np.int64)
+    if seed:
+        slot_block[:, :seed] = np.arange(first, first + seed)
+        block_slot[:, first : first + seed] = np.arange(seed)
+        last_used[:, :seed] = -1
+    return block_slot, slot_block, last_used
 
-    Follows lazykv/tiered.py:389-418 (admit): hits keep their slots and the victims are the least
-    recently used slots outside the chosen set, which with k slots and k chosen blocks is exactly the
-    set of slots the choice does not hit. Victims are taken in ascending slot order by the missed
-    blocks in ascending block order (the reference hands them out in rank order; the order only
-    moves a block between slots, never changes what is attended). Updates block_slot [h, cap] and
-    slot_block [h, k] in place (-1 = empty) and returns loc [h, k]: the slot of a hit, or
+
+def residency_step(block_slot: np.ndarray, slot_block: np.ndarray, last_used: np.ndarray, chosen: np.ndarray, step: int) -> np.ndarray:
+    """One decode step of the hybrid tier's residency, per KV head, over n_slots >= k slots:
+    lazykv/tiered.py:389-418 (admit) followed by the last-use update of gather (:450-452).
+
+    The chosen blocks already in a slot keep it. The victims are the slots the choice does not hit,
+    least recently used first (a stable sort of last_used, so ties go to the lower slot), as many as
+    there are missed blocks, which take them in the order `chosen` lists them. Every slot the step
+    uses, hit or victim, is then last used at `step`. Updates block_slot [h, cap], slot_block
+    [h, n_slots] and last_used [h, n_slots] in place and returns loc [h, k]: the slot of a hit, or
     LOC_MISS | slot for a miss read from the host and copied into that slot.
     """
     h, k = chosen.shape
+    n_slots = slot_block.shape[1]
     loc = np.empty((h, k), dtype=np.int64)
     for j in range(h):
-        cur = block_slot[j, chosen[j]]
-        hit_slots = set(int(s) for s in cur if s >= 0)
-        victims = [s for s in range(slot_block.shape[1]) if s not in hit_slots]
-        order = np.argsort(chosen[j], kind="stable")
-        m = 0
-        for i in order:
-            b = int(chosen[j, i])
-            if cur[i] >= 0:
-                loc[j, i] = cur[i]
-                continue
-            v = victims[m]
-            m += 1
-            old = slot_block[j, v]
-            if old >= 0:
-                block_slot[j, old] = -1
-            slot_block[j, v] = b
-            block_slot[j, b] = v
-            loc[j, i] = LOC_MISS | v
+        row = chosen[j]
+        slots = block_slot[j, row]
+        miss = slots < 0
+        keep = np.zeros(n_slots, dtype=bool)
+        keep[slots[~miss]] = True
+        free = np.flatnonzero(~keep)
+        victims = free[np.argsort(last_used[j, free], kind="stable")[: int(miss.sum())]]
+        want = row[miss]
+        old = slot_block[j, victims]
+        block_slot[j, old[old >= 0]] = -1
+        slot_block[j, victims] = want
+        block_slot[j, want] = victims
+        loc[j, ~miss] = slots[~miss]
+        loc[j, miss] = LOC_MISS | victims
+        last_used[j, block_slot[j, row]] = step
     return loc
+
+
+def slot_order(last_used: np.ndarray) -> np.ndarray:
+    """Each head's slots from least to most recently used, ties to the lower slot: the order in
+    which the reference's stable sort offers them as victims (lazykv/tiered.py:412)."""
+    return np.argsort(last_used, axis=1, kind="stable")

@@ -46,7 +46,7 @@ def test_binding_covers_every_declared_symbol() -> None:
 def test_abi_version_and_record_width(lib) -> None:  # noqa: ANN001
     from oracle import reference as R
 
-    assert lib.lkv_abi_version() == 3
+    assert lib.lkv_abi_version() == 4
     for bs, d in ((16, 64), (16, 128), (8, 64), (64, 64)):
         assert lib.lkv_packed_pair_bytes(bs, d) == R.packed_pair_bytes(bs, d)
 

@@ -1,8 +1,8 @@
 """Parity at the real shapes of the tiered decode workloads, one layer each, against the oracle.
 
 Each case draws a seeded layer (lazykv_amd.workload), builds its tier with the store kernel, then
-checks: the block metadata bit-exact (exact keys, or the dequantised keys of an int8 tier); a
-sample of int8 records bit-exact against the oracle's pack; the selected sets against the
+checks: the block metadata bit-exact (exact keys, or the dequantised keys of an int8 tier); every
+int8 record bit-exact against the oracle's pack; the selected sets against the
 oracle's float64 Quest bound (identical outside near-tie cells) with the planted needle block
 selected for every KV head; and the decode output and LSE within 2e-3 of float64 attention over
 the set the tier attends.
@@ -72,14 +72,16 @@ class _Layer:
             rec = self.records[: self.n_sealed].cpu().numpy()
             self.deq = R.to_f32(R.unpack(rec.reshape(self.n_sealed * H, -1), BS, d, self.dn), self.dn).reshape(self.n_sealed, H, 2, BS, d)
 
-    def check_records_sample(self, count: int = 256) -> None:
-        gen = np.random.default_rng(11)
-        blocks = gen.integers(0, self.n_sealed, count)
-        heads = gen.integers(0, H, count)
-        pairs = _bits(self.pool[torch.from_numpy(blocks).cuda(), torch.from_numpy(heads).cuda()])  # [count, 2, bs, d]
-        want = R.pack(pairs, self.dn)
-        got = self.records[torch.from_numpy(blocks).cuda(), torch.from_numpy(heads).cuda()].cpu().numpy()
-        assert np.array_equal(got, want)
+    def check_records(self, chunk: int = 1024) -> None:
+        """Every sealed (block, head) record against the C oracle's pack of the same pair's bits."""
+        from oracle import quant_c
+
+        for b0 in range(0, self.n_sealed, chunk):
+            b1 = min(self.n_sealed, b0 + chunk)
+            pairs = _bits(self.pool[b0:b1]).reshape((b1 - b0) * H, 2, BS, self.d)  # the records' (block, head) order
+            want = quant_c.pack(pairs, self.dn)
+            got = self.records[b0:b1].cpu().numpy().reshape((b1 - b0) * H, -1)
+            assert np.array_equal(got, want), f"records of blocks {b0}..{b1 - 1}"
 
     def check_metadata(self, source: str) -> None:
         keys = (self.deq if source == "dequantised" else self.exact[: self.n_sealed])[:, :, 0]  # [n_sealed, h, bs, d]
@@ -155,7 +157,7 @@ def test_int8_tier_decode_64k_float16_k1024(where: str) -> None:
     from lazykv_amd.pinned import pinned_empty
 
     layer = _Layer(64, 65536, torch.float16, int8=True, meta_from="dequantised")
-    layer.check_records_sample()
+    layer.check_records()
     layer.check_metadata("dequantised")
     recs = layer.records
     if where == "host":
@@ -196,13 +198,14 @@ def exact_layer():  # noqa: ANN201
 @pytest.mark.parametrize("k", [512, 2048, 4096])
 def test_exact_split_128k_bfloat16(exact_layer, k: int) -> None:  # noqa: ANN001
     """Selected from HBM exactly, the rest from the int8 host tier: the oracle is float64 attention
-    over every token with the unselected sealed blocks dequantised. The deviation from attention
-    over the original values is the int8 tier's error, bounded here loosely."""
+    over every token with the unselected sealed blocks dequantised. Against float64 dense attention
+    over the original values of all 8,192 blocks, the output and LSE must also stay within 2e-3:
+    the int8 tier's error and the kernel's together."""
     from lazykv_amd import kernels
 
     layer, host = exact_layer
     if k == 512:
-        layer.check_records_sample()
+        layer.check_records()
         layer.check_metadata("exact")
     idx = layer.select(k)
     out, lse = _decode(layer, idx, kernels.pool_source(layer.pool), rem=kernels.record_source(host, torch.bfloat16), rem_range=(1, layer.n_sealed))
@@ -218,7 +221,8 @@ def test_exact_split_128k_bfloat16(exact_layer, k: int) -> None:  # noqa: ANN001
     dense_o, dense_l = R.attend_tokens(q, ks, vs, layer.d**-0.5)
     dev_o, dev_l = np.abs(out - dense_o).max(), np.abs(lse - dense_l).max()
     print(f"exact split K={k}: max|out - dense| {dev_o:.2e}, max|lse - dense| {dev_l:.2e}")
-    assert dev_o < 5e-2 and dev_l < 5e-2
+    # The workload's own bar: full dense attention over all 8,192 blocks within 2e-3.
+    assert dev_o < TOL and dev_l < TOL
 
 
 def test_zero_copy_decode_512k_streams_the_selection() -> None:

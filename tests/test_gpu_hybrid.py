@@ -30,19 +30,22 @@ def _layer(seed: int, h: int, g: int, n: int, bs: int, d: int, dt: torch.dtype):
 
 
 @pytest.mark.parametrize(
-    ("h", "g", "n", "bs", "d", "k", "dt", "fill", "quant"),
+    ("h", "g", "n", "bs", "d", "k", "dt", "fill", "quant", "spare"),
     [
-        (8, 4, 300, 16, 128, 32, torch.bfloat16, 16, None),
-        (4, 4, 200, 16, 64, 24, torch.float16, 5, None),
-        (2, 8, 150, 32, 128, 40, torch.bfloat16, 19, None),
-        (8, 4, 300, 16, 128, 32, torch.bfloat16, 16, "int8"),
-        (4, 4, 200, 16, 64, 24, torch.float16, 5, "int8"),
-        (4, 4, 120, 20, 64, 16, torch.float16, 7, "int8"),  # a 4-row tail chunk per pair
-        (2, 8, 100, 64, 128, 20, torch.bfloat16, 50, "int8"),
-        (4, 2, 160, 8, 128, 30, torch.bfloat16, 8, None),
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, 16, None, 0),
+        (4, 4, 200, 16, 64, 24, torch.float16, 5, None, 0),
+        (2, 8, 150, 32, 128, 40, torch.bfloat16, 19, None, 0),
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, 16, "int8", 0),
+        (4, 4, 200, 16, 64, 24, torch.float16, 5, "int8", 0),
+        (4, 4, 120, 20, 64, 16, torch.float16, 7, "int8", 0),  # a 4-row tail chunk per pair
+        (2, 8, 100, 64, 128, 20, torch.bfloat16, 50, "int8", 0),
+        (4, 2, 160, 8, 128, 30, torch.bfloat16, 8, None, 0),
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, 16, None, 32),  # spare slots: twice the selection
+        (4, 4, 200, 16, 64, 24, torch.float16, 5, "int8", 7),
+        (2, 4, 400, 16, 64, 100, torch.bfloat16, 11, None, 1000),  # 1,100 slots: several per thread of the residency launch
     ],
 )
-def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, fill: int, quant: str | None) -> None:
+def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, fill: int, quant: str | None, spare: int) -> None:
     from lazykv_amd import kernels
     from lazykv_amd.pinned import pinned_empty
 
@@ -55,9 +58,9 @@ def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, 
         host = pinned_empty((n, h, recs.shape[1]), torch.uint8)
         host.copy_(recs.reshape(n, h, -1))
         hsrc = kernels.record_source(host, dt)
-    res = kernels.Residency.allocate(k, h, n, bs, d, dt, torch.device("cuda"))
-    bs_ref = np.full((h, n), -1, dtype=np.int64)
-    sb_ref = np.full((h, k), -1, dtype=np.int64)
+    n_slots = k + spare
+    res = kernels.Residency.allocate(k, h, n, bs, d, dt, torch.device("cuda"), n_slots=n_slots)
+    bs_ref, sb_ref, lu_ref = R.residency_state(h, n_slots, n)
     slots_src = pool[[0, n - 1]].contiguous()
     ss = kernels.pool_source(slots_src)
     gen = torch.Generator().manual_seed(5)
@@ -73,14 +76,18 @@ def test_hybrid_decode_is_the_zero_copy_decode(h: int, g: int, n: int, bs: int, 
         assert torch.equal(out_h, out_z) and torch.equal(lse_h, lse_z), step
         chosen = idx.cpu().numpy().astype(np.int64)
         prev = bs_ref.copy()
-        R.residency_step(bs_ref, sb_ref, chosen)
+        R.residency_step(bs_ref, sb_ref, lu_ref, chosen, step)
         assert np.array_equal(res.block_slot.cpu().numpy(), bs_ref), step
         assert np.array_equal(res.slot_block.cpu().numpy(), sb_ref), step
+        assert np.array_equal(res.order.cpu().numpy(), R.slot_order(lu_ref)), step
         hits += int((np.take_along_axis(prev, chosen, axis=1) >= 0).sum())
-        # every slot holds an exact copy of the block the table names
+        # every occupied slot holds an exact copy of the block the table names
         for j in range(h):
-            assert torch.equal(res.slots[:, j], expect[torch.from_numpy(sb_ref[j]).cuda(), j])
+            held = np.flatnonzero(sb_ref[j] >= 0)
+            assert torch.equal(res.slots[torch.from_numpy(held).cuda(), j], expect[torch.from_numpy(sb_ref[j, held]).cuda(), j])
     assert hits > 0  # the drift keeps part of each selection resident
+    if spare:
+        assert (sb_ref >= 0).sum() > h * k  # spare slots keep blocks the current selection does not name
 
 
 @pytest.mark.parametrize(("dt", "d", "u", "scale_bits"), [(torch.float16, 64, 145, 0x01C4), (torch.bfloat16, 128, 185, 0x0989)])
@@ -129,20 +136,26 @@ def test_int8_miss_fill_rounds_like_the_reference(dt: torch.dtype, d: int, u: in
 
 
 @pytest.mark.parametrize(
-    ("h", "g", "n", "bs", "d", "k", "dt", "quant", "mode"),
+    ("h", "g", "n", "bs", "d", "k", "dt", "quant", "mode", "spare", "exact"),
     [
-        (8, 4, 300, 16, 128, 32, torch.bfloat16, None, "f32"),
-        (4, 4, 200, 16, 64, 24, torch.float16, "int8", "f32"),
-        (2, 8, 150, 32, 128, 40, torch.bfloat16, None, "model"),
-        (8, 4, 1200, 16, 64, 200, torch.float16, "int8", "model"),
-        (2, 4, 8194, 16, 64, 512, torch.bfloat16, None, "f32"),  # 8,192 candidates: the largest selected in the residency launch
-        (2, 4, 8300, 16, 64, 512, torch.bfloat16, None, "f32"),  # beyond: the selection takes its own launch
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, None, "f32", 0, False),
+        (4, 4, 200, 16, 64, 24, torch.float16, "int8", "f32", 0, False),
+        (2, 8, 150, 32, 128, 40, torch.bfloat16, None, "model", 0, False),
+        (8, 4, 1200, 16, 64, 200, torch.float16, "int8", "model", 0, False),
+        (2, 4, 8194, 16, 64, 512, torch.bfloat16, None, "f32", 0, False),  # 8,192 candidates: the largest selected in the residency launch
+        (2, 4, 8300, 16, 64, 512, torch.bfloat16, None, "f32", 0, False),  # beyond: the selection takes its own launch
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, None, "f32", 16, False),  # spare slots
+        (4, 4, 200, 16, 64, 24, torch.float16, "int8", "f32", 24, True),  # spare slots and an exact remainder
+        (8, 4, 300, 16, 128, 32, torch.bfloat16, None, "model", 0, True),  # the exact remainder over k slots
+        (2, 4, 8300, 16, 64, 512, torch.bfloat16, None, "f32", 0, True),  # the remainder after the selection's own launch
     ],
 )
-def test_one_call_hybrid_step_is_bound_topk_then_hybrid_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, quant: str | None, mode: str) -> None:
+def test_one_call_hybrid_step_is_bound_topk_then_hybrid_decode(h: int, g: int, n: int, bs: int, d: int, k: int, dt: torch.dtype, quant: str | None, mode: str,
+                                                                spare: int, exact: bool) -> None:
     """lkv_select_hybrid_decode against lkv_bound_topk + lkv_hybrid_decode from the same empty
-    tables over a drifting sequence: the same ids, tables, slot contents, output and LSE, bit for
-    bit, at every step."""
+    tables over a drifting sequence: the same ids, tables, use order, slot contents, output and LSE,
+    bit for bit, at every step. With `exact`, both attend the remainder (every other sealed block,
+    from the host tier), and the two-call output equals lkv_sparse_decode's over the host tier."""
     from lazykv_amd import kernels
     from lazykv_amd.pinned import pinned_empty
 
@@ -155,10 +168,12 @@ def test_one_call_hybrid_step_is_bound_topk_then_hybrid_decode(h: int, g: int, n
         hsrc = kernels.record_source(host, dt)
     rank = kernels._lib.RANK_F32 if mode == "f32" else kernels._lib.RANK_MODEL
     dev = torch.device("cuda")
-    res_a = kernels.Residency.allocate(k, h, n, bs, d, dt, dev)
-    res_b = kernels.Residency.allocate(k, h, n, bs, d, dt, dev)
+    res_a = kernels.Residency.allocate(k, h, n, bs, d, dt, dev, n_slots=k + spare)
+    res_b = kernels.Residency.allocate(k, h, n, bs, d, dt, dev, n_slots=k + spare)
     ss = kernels.pool_source(pool[[0, n - 1]].contiguous())
     common = dict(block_size=bs, scale=d**-0.5, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=bs - 3, out_dtype=torch.float32)
+    if exact:
+        common.update(rem=hsrc, rem_range=(1, n - 1))
     gen = torch.Generator().manual_seed(9)
     q0 = w.query.float()
     idx_b = torch.empty((h, k), dtype=torch.int32, device="cuda")
@@ -167,39 +182,49 @@ def test_one_call_hybrid_step_is_bound_topk_then_hybrid_decode(h: int, g: int, n
         idx_a = kernels.bound_topk(q, kmin, kmax, k, cand_offset=1, n_cand=n - 2, rank_mode=rank)
         out_a, lse_a = kernels.hybrid_decode(q, n_kv=h, host=hsrc, res=res_a, idx=idx_a, **common)
         out_b, lse_b = kernels.select_hybrid_decode(q, kmin, kmax, k, cand_offset=1, n_cand=n - 2, host=hsrc, res=res_b, rank_mode=rank, out_idx=idx_b, **common)
+        if exact:
+            out_z, lse_z = kernels.sparse_decode(q, n_kv=h, sel=hsrc, idx=idx_a, **common)
         torch.cuda.synchronize()
         assert torch.equal(idx_b, idx_a), step
         assert torch.equal(out_b, out_a) and torch.equal(lse_b, lse_a), step
         assert torch.equal(res_b.block_slot, res_a.block_slot) and torch.equal(res_b.slot_block, res_a.slot_block), step
+        assert torch.equal(res_b.order, res_a.order), step
         assert torch.equal(res_b.slots, res_a.slots), step
+        if exact:
+            assert torch.equal(out_a, out_z) and torch.equal(lse_a, lse_z), step
     assert (res_b.block_slot >= 0).any()
 
 
-@pytest.mark.parametrize("tables", ["zeros", "garbage"])
-def test_hybrid_decode_survives_tables_that_disagree(tables: str) -> None:
-    """Tables filled with zeros instead of -1, or with out-of-range and contradictory entries: a
-    hit needs block_slot and slot_block to agree, so every step still equals the zero-copy
-    decode, and after it the selected blocks are resident with consistent tables. (A pair of
-    entries that agree is a residency claim, which no table check can tell from a true one.)"""
+@pytest.mark.parametrize(("tables", "spare"), [("zeros", 0), ("garbage", 0), ("zeros", 5), ("garbage", 5)])
+def test_hybrid_decode_survives_tables_that_disagree(tables: str, spare: int) -> None:
+    """Tables filled with zeros instead of -1, or with out-of-range and contradictory entries, and
+    a use order that is not a permutation of the slots: a hit needs block_slot and slot_block to
+    agree and a bad order is read as ascending slots, so every step still equals the zero-copy
+    decode, and after it the selected blocks are resident with consistent tables and the order is a
+    permutation again. (A pair of entries that agree is a residency claim, which no table check can
+    tell from a true one.)"""
     from lazykv_amd import kernels
 
     h, g, n, bs, d, k = 4, 4, 120, 16, 64, 16
+    n_slots = k + spare
     w, pool, host, kmin, kmax = _layer(5, h, g, n, bs, d, torch.float16)
-    res = kernels.Residency.allocate(k, h, n, bs, d, torch.float16, torch.device("cuda"))
+    res = kernels.Residency.allocate(k, h, n, bs, d, torch.float16, torch.device("cuda"), n_slots=n_slots)
     gen = torch.Generator().manual_seed(9)
     if tables == "zeros":
         res.block_slot.zero_()
         res.slot_block.zero_()
+        res.order.zero_()
     else:  # out-of-range and contradictory entries; no pair that agrees (that would be a residency claim)
-        bsl = torch.randint(-9, k + 9, (h, n), generator=gen, dtype=torch.int32)
-        sbl = torch.randint(-9, n + 9, (h, k), generator=gen, dtype=torch.int32)
+        bsl = torch.randint(-9, n_slots + 9, (h, n), generator=gen, dtype=torch.int32)
+        sbl = torch.randint(-9, n + 9, (h, n_slots), generator=gen, dtype=torch.int32)
         for j in range(h):
-            for s_ in range(k):
+            for s_ in range(n_slots):
                 b = int(sbl[j, s_])
                 if 0 <= b < n and int(bsl[j, b]) == s_:
                     sbl[j, s_] = -5
         res.block_slot.copy_(bsl.cuda())
         res.slot_block.copy_(sbl.cuda())
+        res.order.copy_(torch.randint(-3, n_slots + 3, (h, n_slots), generator=gen, dtype=torch.int32).cuda())
     res.slots.normal_()  # slot contents that no table entry may be trusted to describe
     ss = kernels.pool_source(pool[[0, n - 1]].contiguous())
     hsrc = kernels.pool_source(host)
@@ -216,8 +241,9 @@ def test_hybrid_decode_survives_tables_that_disagree(tables: str) -> None:
         for j in range(h):
             for b in idx[j].cpu().tolist():
                 s_ = int(bsl[j, b])
-                assert 0 <= s_ < k and int(sbl[j, s_]) == b, (step, j, b)
+                assert 0 <= s_ < n_slots and int(sbl[j, s_]) == b, (step, j, b)
                 assert torch.equal(res.slots[s_, j], pool[b, j].cuda())
+            assert sorted(res.order[j].cpu().tolist()) == list(range(n_slots)), (step, j)
 
 
 def test_hybrid_decode_refuses_what_it_cannot_hold() -> None:
@@ -226,18 +252,25 @@ def test_hybrid_decode_refuses_what_it_cannot_hold() -> None:
     h, g, n, bs, d, k = 2, 4, 60, 16, 64, 8
     w, pool, host, kmin, kmax = _layer(1, h, g, n, bs, d, torch.float16)
     idx = kernels.bound_topk(w.query.cuda(), kmin, kmax, k, cand_offset=1, n_cand=n - 2)
-    wrong = kernels.Residency.allocate(k + 1, h, n, bs, d, torch.float16, torch.device("cuda"))
+    wrong = kernels.Residency.allocate(k - 1, h, n, bs, d, torch.float16, torch.device("cuda"))  # fewer slots than selected blocks
     with pytest.raises(ValueError, match="slots"):
         kernels.hybrid_decode(w.query.cuda(), n_kv=h, block_size=bs, scale=d**-0.5, host=kernels.pool_source(host), res=wrong, idx=idx)
     common = dict(cand_offset=1, block_size=bs, scale=d**-0.5, host=kernels.pool_source(host))
     with pytest.raises(ValueError, match="slots"):
         kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, k, n_cand=n - 2, res=wrong, **common)
+    spare = kernels.Residency.allocate(k, h, n, bs, d, torch.float16, torch.device("cuda"), n_slots=k + 4)
+    unordered = kernels.Residency(spare.slots, spare.block_slot, spare.slot_block, None)  # spare slots need the use order
+    with pytest.raises(ValueError, match="use order"):
+        kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, k, n_cand=n - 2, res=unordered, **common)
+    too_many = kernels.Residency.allocate(k, h, n, bs, d, torch.float16, torch.device("cuda"), n_slots=5000)  # past the 4,096-slot limit
+    with pytest.raises(ValueError, match="limit"):
+        kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, k, n_cand=n - 2, res=too_many, **common)
     right = kernels.Residency.allocate(k, h, n, bs, d, torch.float16, torch.device("cuda"))
     with pytest.raises(ValueError, match="candidates"):
         kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, k, n_cand=n, res=right, **common)  # past the metadata
     with pytest.raises(ValueError, match="k="):
         kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, n, n_cand=n - 2, res=right, **common)  # more than the candidates
-    short = kernels.Residency(right.slots, right.block_slot[:, : n - 5].contiguous(), right.slot_block)
+    short = kernels.Residency(right.slots, right.block_slot[:, : n - 5].contiguous(), right.slot_block, right.order)
     with pytest.raises(ValueError, match="residency table"):
         kernels.select_hybrid_decode(w.query.cuda(), kmin, kmax, k, n_cand=n - 2, res=short, **common)
 

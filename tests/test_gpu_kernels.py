@@ -608,21 +608,36 @@ def test_pinned_pool_round_trips_and_the_stream_probe_reads_it() -> None:
 
 def test_install_verifies_the_decode_kernel_and_refuses_unknown_strategies() -> None:
     """install() with the model's head counts checks decode (the HIP kernel, spare storage past the
-    live length) and chunked prefill against a float64 truth first (lazykv/attention.py:214-290);
-    a strategy this library does not have is a hard error."""
+    live length) and chunked prefill against a float64 truth first (lazykv/attention.py:214-290).
+    The reference's strategy names (:44) select the HIP kernel, as the reference's fixtures install
+    them (tests/test_tiered.py:25); a name this library does not have is a hard error, and `attend`
+    refuses it as the reference's does (:113)."""
     from lazykv_amd import attention
 
     chosen, checks = attention.install(None, 32, 8, 128)
     assert chosen == "hip" and len(checks) == 1 and checks[0].ok, checks
     assert checks[0].max_rel_err_decode < 1e-2 and checks[0].max_rel_err_prefill < 1e-2
     assert checks[0].seconds_decode_growing_median > 0
-    assert attention.current_strategy() == ("hip", 0)
+    assert attention.current_strategy() == ("hip", attention.DEFAULT_BUCKET)
     chosen, checks = attention.install("hip", 32, 8, 64)
     assert checks[0].ok, checks
-    with pytest.raises(RuntimeError, match="failed verification"):
-        attention.install("cudnn", 32, 8, 64)
-    with pytest.raises(RuntimeError, match="unknown attention strategy"):
-        attention.install("math")
+    for name in attention.REFERENCE_STRATEGIES:
+        chosen, checks = attention.install(name, 32, 8, 64, bucket=64)
+        assert chosen == name and checks[0].strategy == name and checks[0].ok, checks
+        assert attention.current_strategy() == (name, 64)
+    with pytest.raises(RuntimeError, match="unknown"):
+        attention.install("flash", 32, 8, 64)
+    with pytest.raises(RuntimeError, match="unknown"):
+        attention.install("flash")
+    q = torch.randn(1, 8, 1, 64, device="cuda", dtype=torch.float16)
+    k = torch.randn(1, 2, 32, 64, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError, match="unknown attention strategy"):
+        attention.attend(q, k, k, None, "flash")
+    pinned = attention.current_strategy()[0]  # the last name installed above
+    restore = attention.set_strategy_for_test("efficient")
+    assert attention.current_strategy()[0] == "efficient"
+    restore()
+    assert attention.current_strategy()[0] == pinned
 
 
 def test_attention_seam_refuses_a_mask_and_reads_only_the_live_prefix() -> None:
@@ -630,7 +645,7 @@ def test_attention_seam_refuses_a_mask_and_reads_only_the_live_prefix() -> None:
     external mask (it owns causality), and `attend` over the live prefix of a preallocated store
     whose spare rows hold large values matches the float64 truth within 1e-2 relative, for a decode
     token and for a 17-token chunk. head_dim is 64, the smallest the decode kernel takes (the
-    reference's test uses 16). The startup verification passes for the build's strategy and fails,
+    reference's test uses 16). The startup verification passes under every strategy name and fails,
     without raising, for one the library does not have (lazykv/attention.py:248-266)."""
     from lazykv_amd.attention import _truth, attend, lazykv_attention_forward, verify_strategies
 
@@ -648,7 +663,11 @@ def test_attention_seam_refuses_a_mask_and_reads_only_the_live_prefix() -> None:
         ref = _truth(q, k, v, 64**-0.5)
         got = attend(q, k, v, 64**-0.5).double().cpu()
         assert ((got - ref).abs().max() / ref.abs().max()).item() < 1e-2, q_len
+    from lazykv_amd.attention import STRATEGIES
+
     checks = verify_strategies(8, 2, 64, dtype=torch.float16, probe_ctx=2048, steps=4)
-    assert len(checks) == 1 and checks[0].ok, checks
-    other = verify_strategies(8, 2, 64, dtype=torch.float16, candidates=("cudnn",))
+    assert [c.strategy for c in checks] == list(STRATEGIES) and all(c.ok for c in checks), checks
+    # one kernel behind every name: one measurement, reported under each
+    assert len({(c.max_rel_err_decode, c.seconds_decode_growing_median) for c in checks}) == 1
+    other = verify_strategies(8, 2, 64, dtype=torch.float16, candidates=("flash",))
     assert not other[0].ok and "unknown strategy" in other[0].error

@@ -198,7 +198,7 @@ def test_int8_tier_ingests_turns_and_keeps_decoding(tiny) -> None:  # noqa: ANN0
     kv = [(layer.keys[:, :, :prompt].clone(), layer.values[:, :, :prompt].clone()) for layer in full.layers]
     quest = QuestView(full, k, bs, dense_layers=1, bound_dtype=torch.float32)
     ref, _ = _session(model, quest, first, ids[:, prompt:], turns, answer, 4096)
-    tier = TieredCache(FullGPUCache.from_kv(kv, 512), k, bs, 512, dense_layers=1, quant="int8")
+    tier = TieredCache(FullGPUCache.from_kv(kv, 512), k, bs, 512, dense_layers=1, quant="int8", fetch="zerocopy")
     got, _ = _session(model, tier, first, ids[:, prompt:], turns, answer, 4096)
     assert torch.isfinite(got).all()
     assert (got - ref).abs().max().item() < 0.25

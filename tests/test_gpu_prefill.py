@@ -75,7 +75,7 @@ def test_layer_major_prefill_writes_the_reference_tier(tiny, chunk: int, quant: 
     cfg, model = tiny
     ids = _ids(cfg)
     ref_logits, full = _chunk_major(model, cfg, ids[:, :PROMPT], chunk)
-    got = tiered_prefill(model, ids[:, :PROMPT], chunk, K, BS, CAP, dense_layers=1, quant=quant)
+    got = tiered_prefill(model, ids[:, :PROMPT], chunk, K, BS, CAP, dense_layers=1, quant=quant, fetch="zerocopy")
     assert got.chunks == -(-PROMPT // chunk)
     assert torch.equal(got.last_logits, ref_logits)
     nb, fill = divmod(PROMPT, BS)
@@ -106,7 +106,7 @@ def test_layer_major_prefill_writes_the_reference_tier(tiny, chunk: int, quant: 
         assert np.array_equal(_bits(t.pool[1, :, 1, :fill]), vb[:, nb * BS :])
     assert torch.equal(got.full.layers[0].keys[:, :, :PROMPT], full.layers[0].keys[:, :, :PROMPT])
     # Decode after it, through seals: the same log-probabilities as the chunk-major path's tier.
-    ref = TieredCache(full, K, BS, CAP, dense_layers=1, quant=quant)
+    ref = TieredCache(full, K, BS, CAP, dense_layers=1, quant=quant, fetch="zerocopy")
     cont = ids[:, PROMPT : PROMPT + 40]
     a = _teacher_forced(model, ref, ref_logits, cont)
     b = _teacher_forced(model, got.cache, got.last_logits, cont)
@@ -120,7 +120,7 @@ def test_selecting_layers_never_allocate_in_the_full_cache(tiny) -> None:  # noq
     from lazykv_amd.tiered_prefill import tiered_prefill
 
     cfg, model = tiny
-    got = tiered_prefill(model, _ids(cfg)[:, :PROMPT], 32, K, BS, CAP, dense_layers=1)
+    got = tiered_prefill(model, _ids(cfg)[:, :PROMPT], 32, K, BS, CAP, dense_layers=1, fetch="zerocopy")
     assert got.full.layers[0].is_initialized and got.full.layers[0].get_seq_length() == PROMPT
     assert not any(layer.is_initialized for layer in got.full.layers[1:])
     assert len(got.layer_s) == cfg.num_hidden_layers
@@ -132,7 +132,7 @@ def test_prompt_longer_than_capacity_is_refused(tiny) -> None:  # noqa: ANN001
 
     cfg, model = tiny
     with pytest.raises(ValueError, match="exceeds capacity"):
-        tiered_prefill(model, _ids(cfg)[:, :PROMPT], 32, K, BS, capacity_tokens=64, dense_layers=1)
+        tiered_prefill(model, _ids(cfg)[:, :PROMPT], 32, K, BS, capacity_tokens=64, dense_layers=1, fetch="zerocopy")
 
 
 @torch.inference_mode()
@@ -160,7 +160,7 @@ def test_layer_major_prefill_32k_1b_shape_writes_quant_py_records() -> None:
     model = model.to(dtype=torch.float16).eval()
     gen = torch.Generator(device="cuda").manual_seed(0)
     ids = torch.randint(0, cfg.vocab_size, (1, n), device="cuda", generator=gen)
-    got = tiered_prefill(model, ids, chunk, k, bs, n + 64, dense_layers=0, quant="int8")
+    got = tiered_prefill(model, ids, chunk, k, bs, n + 64, dense_layers=0, quant="int8", fetch="zerocopy")
     full = FullGPUCache(cfg.num_hidden_layers, n)
     out = None
     for s in range(0, n, chunk):

@@ -51,7 +51,7 @@ def test_restored_session_continues_bit_identically(tiny, tmp_path, mid: int, re
 
     cfg, model = tiny
     ids = _ids(cfg)
-    got = tiered_prefill(model, ids[:, :PROMPT], 32, K, BS, CAP, dense_layers=1)
+    got = tiered_prefill(model, ids[:, :PROMPT], 32, K, BS, CAP, dense_layers=1, fetch="zerocopy")
     cache, logits = got.cache, got.last_logits
     for t in range(mid):
         logits = _step(model, cache, ids[:, PROMPT + t : PROMPT + t + 1])
@@ -60,7 +60,7 @@ def test_restored_session_continues_bit_identically(tiny, tmp_path, mid: int, re
     assert stats.bytes_written == path.stat().st_size and stats.bytes_written % snapshot.ALIGN == 0
     header, base = snapshot.read_header(path)
     assert header["length"] == PROMPT + mid and base % snapshot.ALIGN == 0
-    restored, logits2, rstats = snapshot.restore(path, K, CAP, cfg.num_hidden_layers, rebuild=rebuild)
+    restored, logits2, rstats = snapshot.restore(path, K, CAP, cfg.num_hidden_layers, fetch="zerocopy", rebuild=rebuild)
     assert rstats.bytes_read > 0
     assert torch.equal(logits, logits2)
     for i, t in cache.tiers.items():
@@ -87,6 +87,6 @@ def test_snapshot_refuses_the_int8_tier(tiny, tmp_path) -> None:  # noqa: ANN001
     from lazykv_amd.tiered_prefill import tiered_prefill
 
     cfg, model = tiny
-    got = tiered_prefill(model, _ids(cfg)[:, :PROMPT], 32, K, BS, CAP, dense_layers=1, quant="int8")
+    got = tiered_prefill(model, _ids(cfg)[:, :PROMPT], 32, K, BS, CAP, dense_layers=1, quant="int8", fetch="zerocopy")
     with pytest.raises(ValueError, match="int8"):
         snapshot.save(got.cache, got.last_logits, tmp_path / "x.lkv")

@@ -104,7 +104,7 @@ def test_int8_decode_differs_from_the_exact_tier_but_not_wildly() -> None:
     ids = torch.randint(0, cfg.vocab_size, (1, 200), device="cuda", generator=gen)
     logits = {}
     for quant in (None, "int8"):
-        got = tiered_prefill(model, ids[:, :160], 32, 3, BS, 512, dense_layers=1, quant=quant)
+        got = tiered_prefill(model, ids[:, :160], 32, 3, BS, 512, dense_layers=1, quant=quant, fetch="zerocopy")
         rows = [got.last_logits.float()]
         with torch.inference_mode():
             for t in range(160, 200):

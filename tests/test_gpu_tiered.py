@@ -169,7 +169,7 @@ def test_exact_cache_reconstructs_full_attention(quant: str | None) -> None:
     from lazykv_amd.tiered import ExactTieredCache
 
     keys, values, gen = _prompt(3, 1200)
-    cache = ExactTieredCache([(keys.cuda(), values.cuda()), (keys.cuda(), values.cuda())], 10, BS, 2048, dense_layers=1, quant=quant)
+    cache = ExactTieredCache([(keys.cuda(), values.cuda()), (keys.cuda(), values.cuda())], 10, BS, 2048, dense_layers=1, quant=quant, fetch="resident")
     shadow = _Shadow(keys, values, quant)
     for _ in range(3):
         k = torch.randn((1, H, 1, D), generator=gen).to(torch.bfloat16)
@@ -209,7 +209,7 @@ def test_cache_routes_layers_and_counts_like_the_reference() -> None:
     from lazykv_amd.tiered import TieredCache
 
     keys, values, gen = _prompt(4, 700)
-    cache = TieredCache([(keys.cuda(), values.cuda())] * 3, 6, BS, 1024, dense_layers=1)
+    cache = TieredCache([(keys.cuda(), values.cuda())] * 3, 6, BS, 1024, dense_layers=1, fetch="zerocopy")
     assert sorted(cache.tiers) == [1, 2] and cache.get_seq_length(1) == 700 and cache.get_seq_length(0) == 700
     k = torch.randn((1, H, 1, D), generator=gen).to(torch.bfloat16).cuda()
     cache.update(k, k, 1)
@@ -223,18 +223,29 @@ def test_cache_routes_layers_and_counts_like_the_reference() -> None:
 
 
 def test_refusals_match_the_reference() -> None:
-    """lazykv/tiered.py:245-248,269-270,573-577 and lazykv/exact.py:169-176."""
+    """lazykv/tiered.py:245-252,269-270,566-577, lazykv/exact.py:165-176, and
+    tests/test_tiered_int8.py:142-143."""
     from lazykv_amd.tiered import ExactTieredCache, TieredCache, TieredLayer, allocate_host_pools
 
     keys, values, _ = _prompt(5, 300)
     kc, vc = keys.cuda(), values.cuda()
     with pytest.raises(ValueError, match="covers all"):
         TieredLayer(kc, vc, 17, BS, 512)
-    with pytest.raises(ValueError, match="zero-copy"):
+    with pytest.raises(ValueError, match="needs the model"):
         TieredCache([(kc, vc)] * 2, 4, BS, 512, dense_layers=1, prefetch=True)
     with pytest.raises(ValueError, match="zero-copy"):
-        TieredCache([(kc, vc)] * 2, 4, BS, 512, dense_layers=1, record_selection=True)
-    with pytest.raises(ValueError, match="resident"):
+        TieredCache([(kc, vc)] * 2, 4, BS, 512, model=object(), dense_layers=1, fetch="zerocopy", prefetch=True)
+    with pytest.raises(ValueError, match="zero-copy"):
+        TieredCache([(kc, vc)] * 2, 4, BS, 512, dense_layers=1, fetch="zerocopy", record_selection=True)
+    with pytest.raises(ValueError, match="outside this path"):
+        TieredCache([(kc, vc)] * 2, 4, BS, 512, dense_layers=1, fetch="gather", record_selection=True)
+    with pytest.raises(ValueError, match="needs fetch='gather'"):
+        TieredCache([(kc, vc)] * 2, 4, BS, 512, dense_layers=1, fetch="runs", quant="int8")
+    with pytest.raises(ValueError, match="unknown fetch mode"):
+        TieredCache([(kc, vc)] * 2, 4, BS, 512, dense_layers=1, fetch="staged")
+    with pytest.raises(ValueError, match="cannot hold a selection"):
+        TieredLayer(kc, vc, 4, BS, 512, n_slots=3, fetch="gather")
+    with pytest.raises(ValueError, match="zero-copy"):
         ExactTieredCache([(kc, vc)] * 2, 4, BS, 512, dense_layers=1, fetch="zerocopy")
     with pytest.raises(ValueError, match="prefetch"):
         ExactTieredCache([(kc, vc)] * 2, 4, BS, 512, dense_layers=1, prefetch=True)

@@ -349,57 +349,69 @@ def test_excluding_a_block_removes_exactly_that_block() -> None:
 # -- hybrid residency ---------------------------------------------------------------------------------
 
 
-def _lru_reference(steps: list[np.ndarray], n_blocks: int, k: int) -> list[set[int]]:
-    """The reference's admit (lazykv/tiered.py:389-418) for one head: victims are the least recently
-    used slots outside the chosen set (empty slots first, ties to the lower slot); returns the
-    resident block set after each step."""
-    slot_block = [-1] * k
-    last_used = [-2] * k
+def _lru_reference(steps: list[np.ndarray], n_slots: int, seeded: list[int]) -> list[list[int]]:
+    """The reference's residency for one head, written over plain lists (lazykv/tiered.py:274-287
+    seeding, :389-418 admit, :450-452 gather): slot s holds slot_block[s]; a seeded slot was last
+    used at -1 and an empty one at -2; victims are the least recently used slots outside the chosen
+    set, ties to the lower slot, handed to the misses in the order the step lists them. Returns
+    slot_block after each step."""
+    slot_block = list(seeded) + [-1] * (n_slots - len(seeded))
+    last_used = [-1] * len(seeded) + [-2] * (n_slots - len(seeded))
     out = []
     for step, chosen in enumerate(steps):
         where = {b: s for s, b in enumerate(slot_block) if b >= 0}
         keep = {where[b] for b in chosen.tolist() if b in where}
         misses = [b for b in chosen.tolist() if b not in where]
-        free = sorted((s for s in range(k) if s not in keep), key=lambda s: (last_used[s], s))
+        free = sorted((s for s in range(n_slots) if s not in keep), key=lambda s: (last_used[s], s))
         for b, s in zip(misses, free):
             slot_block[s] = b
         for b in chosen.tolist():
             last_used[slot_block.index(b)] = step
-        out.append({b for b in slot_block if b >= 0})
+        out.append(list(slot_block))
     return out
 
 
-def test_residency_step_keeps_hits_and_evicts_exactly_the_unhit_slots() -> None:
-    rng = np.random.default_rng(3)
-    h, n, k = 3, 60, 8
-    block_slot = np.full((h, n), -1, dtype=np.int64)
-    slot_block = np.full((h, k), -1, dtype=np.int64)
-    seqs = [[] for _ in range(h)]
+@pytest.mark.parametrize(("k", "spare", "seed"), [(8, 0, 0), (8, 0, 8), (8, 3, 0), (8, 8, 5), (5, 11, 16)])
+def test_residency_step_keeps_hits_and_evicts_the_least_recently_used(k: int, spare: int, seed: int) -> None:
+    rng = np.random.default_rng(3 + k + spare + seed)
+    h, n = 3, 60
+    n_slots = k + spare
+    seed = min(seed, n_slots)
+    first = n - 2 - seed  # the most recent candidate blocks, as a prompt of n - 1 sealed blocks seeds them
+    block_slot, slot_block, last_used = R.residency_state(h, n_slots, n, first, seed)
+    seqs: list[list[np.ndarray]] = [[] for _ in range(h)]
     chosen = np.stack([np.sort(rng.choice(n, k, replace=False)) for _ in range(h)])
-    for _ in range(40):
-        # drift: each step keeps most of the previous choice
+    for step in range(40):
         nxt = []
-        for j in range(h):
+        for j in range(h):  # drift: each step keeps most of the previous choice
             keep = rng.choice(chosen[j], k - 3, replace=False)
             pool = np.setdiff1d(np.arange(n), keep)
             nxt.append(np.sort(np.concatenate([keep, rng.choice(pool, 3, replace=False)])))
-        prev_bs, prev_sb = block_slot.copy(), slot_block.copy()
+        prev_bs, prev_sb, prev_lu = block_slot.copy(), slot_block.copy(), last_used.copy()
         chosen = np.stack(nxt)
-        loc = R.residency_step(block_slot, slot_block, chosen)
+        loc = R.residency_step(block_slot, slot_block, last_used, chosen, step)
         for j in range(h):
             seqs[j].append(chosen[j])
-            assert set(slot_block[j].tolist()) == set(chosen[j].tolist())  # resident set == chosen set
-            for s in range(k):
-                assert block_slot[j, slot_block[j, s]] == s
-            assert (block_slot[j] >= 0).sum() == k
+            resident = set(slot_block[j][slot_block[j] >= 0].tolist())
+            assert set(chosen[j].tolist()) <= resident
+            for s in range(n_slots):  # the two tables agree
+                if slot_block[j, s] >= 0:
+                    assert block_slot[j, slot_block[j, s]] == s
+            assert (block_slot[j] >= 0).sum() == len(resident)
             hits = [i for i in range(k) if prev_bs[j, chosen[j, i]] >= 0]
             for i in hits:  # a hit keeps its slot and is read from it
                 assert loc[j, i] == prev_bs[j, chosen[j, i]] and not loc[j, i] & R.LOC_MISS
             misses = [i for i in range(k) if i not in hits]
-            victims = sorted(int(loc[j, i]) & ~R.LOC_MISS for i in misses)
-            assert victims == sorted(set(range(k)) - {int(prev_bs[j, chosen[j, i]]) for i in hits})
-            # victims go to the misses in ascending block order, in ascending slot order
-            assert [int(loc[j, i]) & ~R.LOC_MISS for i in sorted(misses, key=lambda i: chosen[j, i])] == victims
+            victims = [int(loc[j, i]) & ~R.LOC_MISS for i in misses]  # in the order the step lists the misses
+            hit_slots = {int(prev_bs[j, chosen[j, i]]) for i in hits}
+            unhit = sorted((s for s in range(n_slots) if s not in hit_slots), key=lambda s: (prev_lu[j, s], s))
+            assert victims == unhit[: len(misses)]  # the least recently used, handed out in order
+            if spare == 0:
+                assert resident == set(chosen[j].tolist())  # k slots: exactly the chosen set
             assert all(prev_sb[j, v] not in chosen[j] for v in victims)
+            used = set(hit_slots) | set(victims)
+            assert all(last_used[j, s] == step for s in used) and all(last_used[j, s] == prev_lu[j, s] for s in set(range(n_slots)) - used)
+            assert np.array_equal(R.slot_order(last_used)[j], sorted(range(n_slots), key=lambda s: (last_used[j, s], s)))
     for j in range(h):
-        assert _lru_reference(seqs[j], n, k)[-1] == set(slot_block[j].tolist())
+        seeded = list(range(first, first + seed))
+        assert _lru_reference(seqs[j], n_slots, seeded)[-1] == slot_block[j].tolist()
