@@ -63,11 +63,37 @@ CASES = [
 
 @pytest.mark.parametrize(("h", "g", "n", "bs", "d", "k", "fill", "dt", "where"), CASES)
 def test_select_decode_equals_the_two_launch_path_and_the_oracle(h: int, g: int, n: int, bs: int, d: int, k: int, fill: int, dt: torch.dtype, where: str) -> None:
+    _check_one_call(h, g, n, bs, d, k, fill, dt, where)
+
+
+# Launches whose decode instance is not a matrix-core one over HBM pairs: a float32 query takes the
+# 8-wave vector instance, which has no selecting form, so the one-call step selects in its own
+# launch and then decodes as the two-call path does; int8 records at head_dim 128 with a group of 4
+# take the 4-wave instance over the HBM plan, which selects inside the launch only up to 16 keys per
+# thread of its 256 (4,096 candidates).
+CASES_OTHER_INSTANCES = [
+    (8, 4, 2048, 16, 64, 512, 16, torch.float16, "hbm", True),
+    (8, 4, 8192, 16, 128, 512, 16, torch.bfloat16, "hbm", True),
+    (2, 2, 700, 16, 128, 50, 7, torch.bfloat16, "hbm", True),
+    (4, 4, 4098, 16, 128, 300, 9, torch.bfloat16, "int8-hbm", False),  # 4,096 candidates: inside, 16 keys per thread
+    (4, 4, 4102, 16, 128, 300, 9, torch.bfloat16, "int8-hbm", False),  # 4,100: the selection's own launch
+]
+
+
+@pytest.mark.parametrize(("h", "g", "n", "bs", "d", "k", "fill", "dt", "where", "q_f32"), CASES_OTHER_INSTANCES)
+def test_select_decode_equals_the_two_launch_path_on_other_instances(h: int, g: int, n: int, bs: int, d: int, k: int, fill: int, dt: torch.dtype,
+                                                                      where: str, q_f32: bool) -> None:
+    _check_one_call(h, g, n, bs, d, k, fill, dt, where, q_f32=q_f32)
+
+
+def _check_one_call(h: int, g: int, n: int, bs: int, d: int, k: int, fill: int, dt: torch.dtype, where: str, q_f32: bool = False) -> None:
+    """lkv_select_decode against lkv_bound_topk + lkv_sparse_decode on one layer: the same ids, the
+    same output bits, and both within the bar of the float64 oracle."""
     from lazykv_amd import kernels
     from lazykv_amd.pinned import pinned_empty
     from lazykv_amd.quant import packed_pair_bytes
 
-    print(f"fused decode case: h={h} g={g} n={n} bs={bs} d={d} k={k} fill={fill} {dt} {where}", flush=True)
+    print(f"fused decode case: h={h} g={g} n={n} bs={bs} d={d} k={k} fill={fill} {dt} {where} q_f32={q_f32}", flush=True)
     w, pool, kmin, kmax = _layer(n * 7 + d + k, h, g, n, bs, d, dt)
     n_cand = n - 2  # blocks 1 .. n - 2; block n - 1 is the current block
     tag = "bf16" if dt == torch.bfloat16 else "f16"
@@ -92,7 +118,7 @@ def test_select_decode_equals_the_two_launch_path_and_the_oracle(h: int, g: int,
             return x[0], x[1]
     slots = pool[[0, n - 1]].contiguous().cuda()
     ss = kernels.pool_source(slots)
-    q = w.query.cuda()
+    q = w.query.float().cuda() if q_f32 else w.query.cuda()
     scale = d**-0.5
     common = dict(block_size=bs, scale=scale, sel=sel, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=fill)
     idx_f = torch.full((h, k), -1, dtype=torch.int32, device="cuda")
