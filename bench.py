@@ -48,7 +48,7 @@ METRIC = "decode-step µs/layer & achieved HBM GB/s (% roofline) at 128K ctx, 6.
 HBM_PEAK_GBPS = 8000.0
 PCIE_PEAK_GBPS = 64.0  # PCIe Gen5 x16, one direction
 N_Q, H, BS = 32, 8, 16
-TRAFFIC_FILE = ROOT / "profiles" / "tiered_decode_128k_pmc_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "pmc_traffic.json"  # rocprofv3 FETCH_SIZE / WRITE_SIZE per kernel, every workload
 
 WORKLOADS = {
     "decode128k": dict(layers=32, tokens=131072, d=128, dtype="bfloat16", k=(512,), kind="host"),
@@ -270,15 +270,17 @@ def step_kernels(fused: bool, in_decode: bool, n_cand: int) -> str:
     return call + f"bound_kernel_mf, {sel}, sparse_decode_kernel, decode_merge_kernel"
 
 
-def pmc_traffic() -> dict:
-    """Calibrated HBM/fabric bytes per launch, per "<leg>/<kernel>", from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary of the default workload (a counter run cannot time itself)."""
-    return {key: v["traffic_bytes"] for key, v in _pmc_file().get("kernels", {}).items()}
+def pmc_traffic(workload: str) -> dict:
+    """Calibrated HBM/fabric bytes per launch, per "<leg>/<kernel>", for `workload`, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (a counter run cannot time itself, so
+    separate runs of the same step supply them)."""
+    prefix = workload + "/"
+    return {key[len(prefix):]: v["traffic_bytes"] for key, v in _pmc_file().get("kernels", {}).items() if key.startswith(prefix)}
 
 
-def pmc_run(leg: str) -> str | None:
-    """The profiler command whose counters `pmc_traffic` reports for a leg."""
-    return _pmc_file().get("runs", {}).get(leg)
+def pmc_run(workload: str, leg: str) -> str | None:
+    """The profiler command whose counters `pmc_traffic` reports for a workload's leg."""
+    return _pmc_file().get("runs", {}).get(f"{workload}/{leg}")
 
 
 def cpu_cores() -> tuple[int, int]:
@@ -592,28 +594,29 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
         "step_stats": dict(m["step_stats"], note="each step replayed between events of its own, after the timed region"),
     }
     # The dominant kernel is lkv_sparse_decode (sparse_decode_kernel + decode_merge_kernel).
-    traffic = pmc_traffic() if kind == "host" else {}
+    traffic = pmc_traffic(args.workload)
+    traffic_note = {}
+    if traffic.get(f"{main_leg}/sparse_decode_kernel"):
+        traffic_note = {"traffic_note": "calibrated FETCH_SIZE + WRITE_SIZE bytes per launch, host (PCIe) and HBM fetches together; algorithmic total incl. HBM part "
+                                        f"{m['sparse_decode_pcie_bytes'] + m['sparse_decode_hbm_bytes']}; source {TRAFFIC_FILE.relative_to(ROOT)}",
+                        "traffic_run": pmc_run(args.workload, main_leg)}
     if m["sparse_decode_pcie_bytes"]:
         gbps = m["sparse_decode_pcie_gbps"]
         kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H))
                  else "sparse_decode_kernel + decode_merge_kernel")
         out["roofline"] = {"bound": "pcie", "kernel": f"{kname}, host reads over PCIe", "achieved": gbps,
-                           "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get("zerocopy/sparse_decode_kernel"),
-                           "algorithmic_bytes": m["sparse_decode_pcie_bytes"], "kernel_us": m["sparse_decode_us"]}
+                           "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get(f"{main_leg}/sparse_decode_kernel"),
+                           "algorithmic_bytes": m["sparse_decode_pcie_bytes"], "kernel_us": m["sparse_decode_us"], **traffic_note}
         if probe.get("dma_h2d_gbps"):
             out["roofline"]["link_ceiling_gbps"] = round(probe["dma_h2d_gbps"], 2)  # the copy engines over the same pool
             out["roofline"]["frac_of_link_ceiling"] = round(gbps / probe["dma_h2d_gbps"], 4)
-        if traffic:
-            out["roofline"]["traffic_note"] = ("calibrated FETCH_SIZE + WRITE_SIZE bytes per launch, host (PCIe) and HBM fetches together; algorithmic total incl. HBM part "
-                                               f"{m['sparse_decode_pcie_bytes'] + m['sparse_decode_hbm_bytes']}; source {TRAFFIC_FILE.relative_to(ROOT)}")
-            out["roofline"]["traffic_run"] = pmc_run("zerocopy")
     else:
         gbps = m["sparse_decode_hbm_gbps"]
         kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H))
                  else "sparse_decode_kernel + decode_merge_kernel")
         out["roofline"] = {"bound": "hbm", "kernel": f"{kname}, HBM", "achieved": gbps,
-                           "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get("hbm/sparse_decode_kernel"),
-                           "algorithmic_bytes": m["sparse_decode_hbm_bytes"], "kernel_us": m["sparse_decode_us"]}
+                           "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get(f"{main_leg}/sparse_decode_kernel"),
+                           "algorithmic_bytes": m["sparse_decode_hbm_bytes"], "kernel_us": m["sparse_decode_us"], **traffic_note}
     out["byte_roofline"] = {"hbm_bytes_per_layer": m["hbm_bytes_per_layer"], "pcie_bytes_per_layer": m["pcie_bytes_per_layer"],
                             "t_roof_us_at_64gbps": m["t_roof_us"], "frac_at_64gbps": m["frac"],
                             "t_roof_us_at_probe": m["t_roof_us_at_probe"], "frac_at_probe": m["frac_at_probe"]}
@@ -629,6 +632,7 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
     if kind == "host" and "hbm" in legs_out:
         hb = legs_out["hbm"]
         out["hbm_resident"] = {"us_per_layer": hb["us_per_layer"], "ms_per_step": hb["ms_per_step"], "hbm_bytes_per_layer": hb["hbm_bytes_per_layer"],
+                               "decode_traffic": traffic.get("hbm/sparse_decode_kernel"),
                                "t_roof_us": hb["t_roof_us"], "frac": hb["frac"], "bound_us_per_launch": hb["bound_graph_us"], "bound_gbps": hb["bound_graph_gbps"],
                                "bound_topk_launch_inclusive_us": hb["bound_topk_us"],
                                "sparse_decode_us": hb["sparse_decode_us"], "sparse_decode_gbps": hb["sparse_decode_hbm_gbps"]}
@@ -937,7 +941,7 @@ def run_prefill(args: argparse.Namespace, spec: dict) -> dict:
                                  "chunk while the next chunk computes; the launch shares the GPU with that compute"},
         "roofline": {"bound": "pcie", "kernel": "store_blocks_kernel (int8 records to host + metadata of the dequantised keys), one launch per chunk in the prefill",
                      "achieved": round(pcie_in, 2), "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(pcie_in / PCIE_PEAK_GBPS, 4),
-                     "traffic": pmc_traffic().get("prefill/store_blocks_kernel"),
+                     "traffic": pmc_traffic(args.workload).get("prefill/store_blocks_kernel"),
                      "traffic_note": f"calibrated FETCH_SIZE + WRITE_SIZE bytes per launch (K/V read + records and metadata written), algorithmic per layer "
                                      f"{b_read + b_rec + b_meta}; source {TRAFFIC_FILE.relative_to(ROOT)}",
                      "algorithmic_bytes": b_rec // launches, "kernel_us": round(boundary_us / launches, 2), "launches_per_layer": launches,

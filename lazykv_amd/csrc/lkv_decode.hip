@@ -1365,6 +1365,34 @@ __device__ __forceinline__ uint32_t res_block_scan(uint32_t v, uint32_t* slots, 
   return before + x - v;
 }
 
+// Two exclusive prefix sums over the workgroup's threads in one barrier (slots_a, slots_b: one
+// word per wave each).
+__device__ __forceinline__ void res_block_scan2(uint32_t va, uint32_t vb, uint32_t* slots_a, uint32_t* slots_b, uint32_t* before_a,
+                                                uint32_t* before_b, uint32_t* total_a, uint32_t* total_b) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t xa = lkv::wave_inclusive_sum(va), xb = lkv::wave_inclusive_sum(vb);
+  if (lane == 63) {
+    slots_a[wave] = xa;
+    slots_b[wave] = xb;
+  }
+  __syncthreads();
+  uint32_t ba = 0, bb = 0, ta = 0, tb = 0;
+#pragma unroll
+  for (int w = 0; w < kResThreads / 64; ++w) {
+    const uint32_t a = slots_a[w], b = slots_b[w];
+    if (w < wave) {
+      ba += a;
+      bb += b;
+    }
+    ta += a;
+    tb += b;
+  }
+  *before_a = ba + xa - va;
+  *before_b = bb + xb - vb;
+  *total_a = ta;
+  *total_b = tb;
+}
+
 // The selection a residency launch makes first (SEL): the k highest of the head's n_cand bounds,
 // by lkv_bound_topk's rule, written ascending to `ids` for the decode launch.
 struct ResSelect {
@@ -1395,7 +1423,8 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
                                                                 ResTables t, int32_t* __restrict__ loc, int64_t loc_stride,
                                                                 ResSelect rs) {
   __shared__ uint32_t hit[kMaxSlots / 32];
-  __shared__ uint32_t used[kMaxSlots / 32];  // hit or taken as a victim this step; first: the order's validity check
+  __shared__ uint32_t seen[kMaxSlots / 32];  // slots the order names once (the order's validity check)
+  __shared__ uint32_t used[kMaxSlots / 32];  // hit or taken as a victim this step
   __shared__ int32_t victims[kMaxSlots];
   __shared__ uint32_t scan_a[kResThreads / 64], scan_b[kResThreads / 64];
   using SelLds = typename std::conditional<SEL, lkv::SelectLds<kResThreads, kResSelKpt>, char>::type;
@@ -1460,6 +1489,7 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   const int32_t* idx_h = idx + (int64_t)h * idx_stride;
   for (int i = threadIdx.x; i < kMaxSlots / 32; i += kResThreads) {
     hit[i] = 0u;
+    seen[i] = 0u;
     used[i] = 0u;
   }
   if (cached) {
@@ -1479,28 +1509,7 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
     const int i = threadIdx.x + u * kResThreads;
     if (i < n_slots) s_order[i] = to[u];
   }
-  __syncthreads();
-  // The order must name every slot once. Count first occurrences of in-range entries; anything
-  // short of n_slots (an entry out of range or repeated) and the head's order is ascending slots.
-  uint32_t firsts = 0u;
-#pragma unroll
-  for (int u = 0; u < kTs; ++u) {
-    const int i = threadIdx.x + u * kResThreads;
-    const int sl = i < n_slots ? s_order[i] : -1;
-    if (sl >= 0 && sl < n_slots && !(atomicOr(&used[sl >> 5], 1u << (sl & 31)) & (1u << (sl & 31)))) ++firsts;
-  }
-  uint32_t n_firsts;
-  res_block_scan(firsts, scan_a, &n_firsts);
-  const bool order_ok = (int)n_firsts == n_slots;
-  if (!order_ok) {
-    // Not a permutation: ascending slot order. Every thread reads its positions from here on.
-#pragma unroll
-    for (int u = 0; u < kTs; ++u) {
-      const int i = threadIdx.x + u * kResThreads;
-      if (i < n_slots) s_order[i] = i;
-    }
-  }
-  for (int i = threadIdx.x; i < kMaxSlots / 32; i += kResThreads) used[i] = 0u;
+  __syncthreads();  // the tables in LDS, the bitmaps cleared
   // This thread's items [i0, i0 + per): their blocks and current slots.
   int32_t blk[kResPer], cur[kResPer];
 #pragma unroll
@@ -1515,36 +1524,65 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   // left inconsistent (or filled with zeros instead of -1) can then cost misses, never a read of
   // a slot that holds another block. Distinct blocks therefore hit distinct slots.
 #pragma unroll
-  for (int u = 0; u < kResPer; ++u)
+  for (int u = 0; u < kResPer; ++u) {
     if (cur[u] >= 0 && (cached ? s_sblock[cur[u]] : sblock_h[cur[u]]) != blk[u]) cur[u] = -1;
-  __syncthreads();  // the order is settled and `used` cleared
-#pragma unroll
-  for (int u = 0; u < kResPer; ++u)
     if (cur[u] >= 0) atomicOr(&hit[cur[u] >> 5], 1u << (cur[u] & 31));
-  __syncthreads();
-  // Victim candidates: the unhit slots in least-recently-used order. Thread t owns order positions
-  // [t*ps, t*ps + ps).
-  uint32_t free_mask = 0u;
+  }
+  // This thread's order positions [s0, s0 + ps): each the first naming of its slot (the order must
+  // name every slot once), and those slots' LDS marks.
   int32_t oslot[kResPer];
+  uint32_t first_mask = 0u;
 #pragma unroll
   for (int u = 0; u < kResPer; ++u) {
     const int p = s0 + u;
     oslot[u] = (u < ps && p < n_slots) ? s_order[p] : -1;
-    const bool in = oslot[u] >= 0 && !((hit[oslot[u] >> 5] >> (oslot[u] & 31)) & 1u);
-    free_mask |= (in ? 1u : 0u) << u;
+    const int sl = oslot[u];
+    const bool first = sl >= 0 && sl < n_slots && !(atomicOr(&seen[sl >> 5], 1u << (sl & 31)) & (1u << (sl & 31)));
+    first_mask |= (first ? 1u : 0u) << u;
   }
-  uint32_t n_free;
-  uint32_t vpos = res_block_scan(__popc(free_mask), scan_a, &n_free);
+  __syncthreads();  // the hits and the first namings are complete
+  // Victim candidates: the unhit slots in least-recently-used order (a slot counts at its first
+  // naming only), and the misses in ascending item order -- two scans in one barrier. With an
+  // order that is not a permutation every position's slot is counted as a first naming short of
+  // n_slots, and the order is read as ascending slots instead (below).
+  uint32_t free_mask = 0u, miss_mask = 0u;
+#pragma unroll
+  for (int u = 0; u < kResPer; ++u) {
+    const int sl = oslot[u];
+    const bool in = ((first_mask >> u) & 1u) && !((hit[sl >> 5] >> (sl & 31)) & 1u);
+    free_mask |= (in ? 1u : 0u) << u;
+    miss_mask |= (cur[u] == -1 ? 1u : 0u) << u;
+  }
+  const uint32_t n_first_local = __popc(first_mask);
+  uint32_t vpos, mpos, n_free, n_miss;
+  // scan_a carries the free counts in its low 16 bits and the first namings in its high 16 (both
+  // at most 4,096 per head).
+  res_block_scan2((n_first_local << 16) | __popc(free_mask), __popc(miss_mask), scan_a, scan_b, &vpos, &mpos, &n_free, &n_miss);
+  const bool order_ok = (int)(n_free >> 16) == n_slots;
+  vpos &= 0xffffu;
+  n_free &= 0xffffu;
+  if (!order_ok) {
+    // Not a permutation of the slots: ascending slot order, free slots counted again.
+    __syncthreads();  // every thread has read the scan words
+#pragma unroll
+    for (int u = 0; u < kResPer; ++u) {
+      const int p = s0 + u;
+      oslot[u] = (u < ps && p < n_slots) ? p : -1;
+      if (oslot[u] >= 0) s_order[p] = p;
+    }
+    free_mask = 0u;
+#pragma unroll
+    for (int u = 0; u < kResPer; ++u) {
+      const int sl = oslot[u];
+      free_mask |= (sl >= 0 && !((hit[sl >> 5] >> (sl & 31)) & 1u) ? 1u : 0u) << u;
+    }
+    vpos = res_block_scan(__popc(free_mask), scan_a, &n_free);
+  }
 #pragma unroll
   for (int u = 0; u < kResPer; ++u) {
     if ((free_mask >> u) & 1u) victims[vpos++] = oslot[u];
   }
-  // Misses, ordinal in ascending item (= block) order.
-  uint32_t miss_mask = 0u;
-#pragma unroll
-  for (int u = 0; u < kResPer; ++u) miss_mask |= (cur[u] == -1 ? 1u : 0u) << u;
-  uint32_t n_miss;
-  uint32_t mpos = res_block_scan(__popc(miss_mask), scan_b, &n_miss);  // its barrier also publishes `victims`
+  __syncthreads();  // the victims are published
   int32_t* loc_h = loc + (int64_t)h * loc_stride;
 #pragma unroll
   for (int u = 0; u < kResPer; ++u) {
@@ -1575,15 +1613,15 @@ __global__ __launch_bounds__(kResThreads) void residency_kernel(const int32_t* _
   uint32_t keep_mask = 0u, use_mask = 0u;
 #pragma unroll
   for (int u = 0; u < kResPer; ++u) {
-    const bool kept = oslot[u] >= 0 && !((used[oslot[u] >> 5] >> (oslot[u] & 31)) & 1u);
+    const bool kept = oslot[u] >= 0 && !((used[oslot[u] >> 5] >> (oslot[u] & 31)) & 1u) && (!order_ok || ((first_mask >> u) & 1u));
     keep_mask |= (kept ? 1u : 0u) << u;
     const int sl = s0 + u;
     const bool usd = u < ps && sl < n_slots && ((used[sl >> 5] >> (sl & 31)) & 1u);
     use_mask |= (usd ? 1u : 0u) << u;
   }
-  uint32_t n_kept, n_used;
-  uint32_t kpos = res_block_scan(__popc(keep_mask), scan_a, &n_kept);
-  uint32_t upos = res_block_scan(__popc(use_mask), scan_b, &n_used) + n_kept;
+  uint32_t kpos, upos, n_kept, n_used;
+  res_block_scan2(__popc(keep_mask), __popc(use_mask), scan_a, scan_b, &kpos, &upos, &n_kept, &n_used);
+  upos += n_kept;
 #pragma unroll
   for (int u = 0; u < kResPer; ++u) {
     if ((keep_mask >> u) & 1u) order_h[kpos++] = oslot[u];
