@@ -821,6 +821,24 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
     pair = packed_pair_bytes(BS, d) if int8 else 2 * BS * d * torch.tensor([], dtype=dtype).element_size()
     miss_bytes = (1.0 - hit_rate) * H * k * pair
     log(f"hybrid128k: hybrid {warm_h:.1f} us/layer (cold step {t_h[0]:.1f}), zero-copy {warm_z:.1f} us/layer, hit rate {hit_rate:.3f}")
+    step_gbps = miss_bytes / (warm_h * 1e-6) / 1e9
+    roofline = {"bound": "pcie", "kernel": "the whole lkv_select_hybrid_decode call per layer (bound_kernel_mf, residency_kernel choosing the top K, "
+                                            "sparse_decode_kernel reading hits from HBM slots and misses over PCIe, decode_merge_kernel)",
+                "achieved": round(step_gbps, 2), "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(step_gbps / PCIE_PEAK_GBPS, 4), "traffic": None,
+                "algorithmic_bytes": int(miss_bytes), "step_us": round(warm_h, 2),
+                "note": "the missed pairs' host bytes per layer over the warm steps' mean call time, launches and gaps included; the call is "
+                        "one C entry point, so its decode launch is not timed apart here (its kernel-trace duration is in profiles/)"}
+    wl = "hybrid128k_int8" if int8 else "hybrid128k"
+    counted = _pmc_file().get("kernels", {}).get(f"{wl}/hybrid/sparse_decode_kernel")
+    if counted:
+        roofline["traffic"] = counted["traffic_bytes"]
+        roofline["traffic_note"] = ("calibrated FETCH_SIZE + WRITE_SIZE bytes per hybrid decode launch: hits read from HBM slots, misses read over "
+                                    f"PCIe and written into their slots; algorithmic {counted['algorithmic_bytes']} at that run's hit rate "
+                                    f"{counted['hit_rate']}; source {TRAFFIC_FILE.relative_to(ROOT)}")
+        roofline["traffic_run"] = pmc_run(wl, "hybrid")
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_hybrid(layers, q_seq, k, n_sealed, fill, d**-0.5, args.cpu_seconds, int8, dtype, n_cand)
     return {
         "metric": "hybrid residency decode-step µs/layer over a drifting decode sequence, against the zero-copy read of the same sequence",
         "value": round(warm_h, 3), "unit": "us/layer", "n_gpus": 1, "steps": S - 1, "warmup": 1,
@@ -837,6 +855,56 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
         "outputs_equal_zerocopy": True,
         "step_calls": "one lkv_select_hybrid_decode call per layer (bound, top K chosen in the residency launch, decode, merge: 4 launches) "
                       "against one lkv_select_decode call (bound, decode choosing the top K, merge: 3 launches)",
+        "roofline": roofline,
+        **({"cpu_baseline": cpu} if cpu is not None else {}),
+    }
+
+
+def cpu_baseline_hybrid(layers: list, q_seq, k: int, n_sealed: int, fill: int, scale: float, budget_s: float, int8: bool, dtype, n_cand: int) -> dict:  # noqa: ANN001
+    """The hybrid tier's step on the CPU (oracle.cpu_path.hybrid_layer), each sampled layer stepping
+    through the same drifting query sequence with its own slots and residency tables, beside the
+    GPU's layer-0 output for the sequence's first query."""
+    import torch
+
+    from lazykv_amd import kernels
+    from oracle import cpu_path
+    from oracle.reference import residency_state
+
+    n_layers = min(len(layers), 2)
+    S = q_seq.shape[0]
+    states = []
+    for li in range(n_layers):
+        st = layers[li]
+        h, bs, d = st["kmin"].shape[1], st["slots"].shape[3], st["slots"].shape[-1]
+        states.append(({"q": q_seq[:, li].cpu(), "kmin": st["kmin"].cpu(), "kmax": st["kmax"].cpu(), "host": st["host"],
+                        "slots": torch.zeros((k, h, 2, bs, d), dtype=dtype), "res": residency_state(h, k, st["kmin"].shape[2]), "t": 0,
+                        "sink": st["slots"][0].cpu(), "cur": st["slots"][1].cpu()},))
+
+    def step(c: dict) -> tuple:
+        t = c["t"]
+        c["t"] = t + 1
+        return cpu_path.hybrid_layer(c["q"][t % S], c["kmin"], c["kmax"], n_sealed, k, c["host"], c["slots"], c["res"], t, c["sink"], c["cur"], fill, scale)
+
+    # Parity beside the timing: layer 0's first step (empty slots) against the GPU's float32 output
+    # for the same query, which the hybrid call equals bit for bit (the bench asserts it per step).
+    st0 = layers[0]
+    ss0 = kernels.pool_source(st0["slots"])
+    o32, l32 = kernels.select_decode(q_seq[0, 0], st0["kmin"], st0["kmax"], k, cand_offset=1, n_cand=n_cand, block_size=BS, scale=scale, sel=st0["hs"],
+                                     sink=ss0, sink_block=0, cur=ss0, cur_block=1, fill=fill, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    r0 = step(states[0][0])
+    parity = {"gpu_vs_cpu_layer0_max_abs_out_f32": float((r0[0] - o32.cpu()).abs().max()),
+              "gpu_vs_cpu_layer0_max_abs_lse": float((r0[1] - l32.cpu()).abs().max()), "parity_bar": 2e-3}
+    t = time_cpu(step, states, budget_s)
+    return {
+        "value": round(t["median_s"] * 1e6, 1), "unit": "us/layer", "cores": t["cores"], "kind": "port",
+        "sample": f"{t['runs']} single-layer hybrid steps of layers 0-{n_layers - 1} of the same workload, each layer stepping through the "
+                  f"{S}-query drifting sequence with its own {k} slots per head: fp32 quest bound, topk, admit (LRU victims, "
+                  f"index_copy of the missed {'int8 records, unpacked' if int8 else 'pairs'} from the host pool into the slots), "
+                  f"index_select gather from the slots, cat, masked fp32 attention + logsumexp (median over {t['runs_at_cores']} at "
+                  f"{t['cores']} threads), torch CPU ops in the reference's order",
+        "iqr_us": [round(x * 1e6, 1) for x in t["iqr_s"]], "per_thread_setting_us": t["per_thread_setting_us"],
+        "cpu_model": cpu_model(), "host_cpus_visible": t["avail"], **parity,
     }
 
 

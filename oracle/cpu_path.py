@@ -15,8 +15,9 @@ It keeps the reference's algorithm and op order, in torch CPU ops:
 
 The other workloads' CPU paths follow the same rule: `decode_layer_int8` (the int8 tier: gather
 records, `unpack`, attend), `exact_layer` (the exact tier: the gathered partial plus the batched,
-masked CPU partial over the float32 mirror, merged by log-sum-exp) and `tier_build_layer` (the
-int8 boundary: `pack`, `unpack`, key min/max).
+masked CPU partial over the float32 mirror, merged by log-sum-exp), `hybrid_layer` (the hybrid
+residency tier: rank, admit the missed blocks into the least recently used slots, gather from the
+slots, attend) and `tier_build_layer` (the int8 boundary: `pack`, `unpack`, key min/max).
 """
 
 from __future__ import annotations
@@ -64,6 +65,75 @@ def decode_layer(
     lse = torch.logsumexp(scores, dim=-1)
     out = torch.softmax(scores, dim=-1) @ values.float()
     return out.reshape(n_q, d), lse.reshape(n_q), top[0]
+
+
+def _rank(query: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, n_full: int, k: int) -> tuple[torch.Tensor, int, int, int]:
+    """Quest's bound over candidates 1..n_full-1 and each head's top k, in descending bound order
+    (lazykv/selection.py:46-62 ranked in float32, +1 at lazykv/tiered.py:386)."""
+    h, d = kmin.shape[1], kmin.shape[-1]
+    g = query.shape[0] // h
+    q = query.float().view(1, h, g, d)
+    qp = q.clamp_min(0)
+    bound = (qp @ kmax[:, :, 1:n_full].float().transpose(-1, -2)) + ((q - qp) @ kmin[:, :, 1:n_full].float().transpose(-1, -2))
+    return bound.amax(dim=2).topk(k, dim=-1).indices[0] + 1, h, g, d
+
+
+def _attend(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, bs: int, fill: int, scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Explicit float32 attention with its LSE over [h, total, d], the last block masked past fill."""
+    total = keys.shape[1]
+    mask = torch.zeros(total)
+    mask[total - bs + fill :] = float("-inf")
+    scores = (q @ keys.float().transpose(-1, -2)) * scale + mask
+    return torch.softmax(scores, dim=-1) @ values.float(), torch.logsumexp(scores, dim=-1)
+
+
+def hybrid_layer(
+    query: torch.Tensor,
+    kmin: torch.Tensor,
+    kmax: torch.Tensor,
+    n_full: int,
+    k: int,
+    host_pool: torch.Tensor,
+    slot_pool: torch.Tensor,
+    residency: tuple,
+    step: int,
+    sink: torch.Tensor,
+    current: torch.Tensor,
+    fill: int,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One decode step of the hybrid residency tier (rung 6), in the reference's order: rank
+    (lazykv/tiered.py:383-387), admit the missed (head, block) pairs into the least recently used
+    slots the choice does not hit, copying them from the host pool (:389-449; an int8 record is
+    widened on arrival, :428-432), then gather sink, the chosen blocks from their slots in rank
+    order and the current block (:450-470), and attend.
+
+    host_pool [cap, h, 2, bs, d] (or int8 records [cap, h, P]); slot_pool [n_slots, h, 2, bs, d];
+    residency = (block_slot, slot_block, last_used) as `reference.residency_state` builds them,
+    updated in place by `reference.residency_step`. Returns (out [n_q, d], lse [n_q], chosen [h, k]).
+    """
+    from oracle.reference import LOC_MISS, residency_step
+
+    top, h, g, d = _rank(query, kmin, kmax, n_full, k)
+    bs = sink.shape[2]
+    chosen = top.numpy()
+    loc = residency_step(*residency, chosen, step)
+    heads = torch.arange(h)[:, None].expand(h, k)
+    miss = torch.from_numpy((loc & LOC_MISS) != 0)
+    slot = torch.from_numpy(loc & ~LOC_MISS)
+    if bool(miss.any()):
+        src = (top[miss] * h + heads[miss]).reshape(-1)
+        dst = (slot[miss] * h + heads[miss]).reshape(-1)
+        flat = host_pool.reshape(host_pool.shape[0] * h, -1)
+        arrived = flat.index_select(0, src)
+        if host_pool.dtype == torch.uint8:
+            arrived = unpack_records(arrived, bs, d, slot_pool.dtype)
+        slot_pool.view(-1, 2, bs, d).index_copy_(0, dst, arrived.view(-1, 2, bs, d))
+    sel = slot_pool.view(-1, 2, bs, d).index_select(0, (slot * h + heads).reshape(-1)).view(h, k, 2, bs, d)
+    keys = torch.cat([sink[:, None, 0], sel[:, :, 0], current[:, None, 0]], dim=1).view(h, (k + 2) * bs, d)
+    values = torch.cat([sink[:, None, 1], sel[:, :, 1], current[:, None, 1]], dim=1).view(h, (k + 2) * bs, d)
+    out, lse = _attend(query.float().view(h, g, d), keys, values, bs, fill, scale)
+    return out.reshape(-1, d), lse.reshape(-1), top
 
 
 # -- int8 tier, exact split and the tier build: the reference's torch ops on CPU tensors ------------

@@ -114,3 +114,36 @@ def test_cpu_exact_layer_is_full_attention() -> None:
     want_o, want_l = R.attend_tokens(query.double().numpy(), ks, vs, D**-0.5)
     assert np.abs(out.numpy() - want_o).max() < 1e-4
     assert np.abs(lse.numpy() - want_l).max() < 1e-4
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_cpu_hybrid_layer_decodes_like_the_zero_copy_path(int8: bool) -> None:
+    """Over a drifting query sequence, the hybrid step attends exactly what the zero-copy step
+    attends (the same blocks, read from slots that hold the host pool's pairs, or the records
+    dequantised), so out, LSE and the chosen ids are equal bit for bit; after each step every
+    resident slot holds its block, and the slots the step names are the chosen blocks'."""
+    n_full, k, fill, steps = 40, 6, 9, 8
+    keys, values, pool, kmin, kmax, query = _state(11, n_full, fill)
+    host = C.pack_pairs(pool.reshape(-1, 2, BS, D)).view(pool.shape[0], H, -1) if int8 else pool
+    widened = C.unpack_records(host.reshape(-1, host.shape[-1]), BS, D, pool.dtype).view(pool.shape) if int8 else pool
+    sink, cur = widened[0], widened[n_full]
+    slots = torch.zeros((k, H, 2, BS, D), dtype=pool.dtype)
+    res = R.residency_state(H, k, pool.shape[0])
+    gen = torch.Generator().manual_seed(3)
+    misses = []
+    for t in range(steps):
+        q = (query.float() + 0.5 * torch.randn(query.shape, generator=gen)).to(query.dtype)
+        before = res[0].copy()
+        out, lse, top = C.hybrid_layer(q, kmin, kmax, n_full, k, host, slots, res, t, sink, cur, fill, D**-0.5)
+        zc = (C.decode_layer_int8 if int8 else C.decode_layer)(q, kmin, kmax, n_full, k, host, sink, cur, fill, D**-0.5)
+        assert torch.equal(out, zc[0]) and torch.equal(lse, zc[1]) and torch.equal(top, zc[2]), t
+        block_slot, slot_block, last_used = res
+        for j in range(H):
+            for s in range(k):
+                b = int(slot_block[j, s])
+                if b >= 0:
+                    assert torch.equal(slots[s, j], widened[b, j]), (t, j, s)
+            assert sorted(block_slot[j, top[j].numpy()].tolist()) == list(range(k))  # k slots hold exactly the choice
+            assert (last_used[j] == t).all()
+        misses.append(int((np.take_along_axis(before, top.numpy(), axis=1) < 0).sum()))
+    assert misses[0] == H * k and 0 < sum(misses[1:]) < (steps - 1) * H * k  # some hits, some misses
