@@ -1158,6 +1158,46 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const float* __restri
   }
 }
 
+// The merge for at most NS partials (NS <= 64): one wave per query head, with no LDS and no
+// barrier. Lane s holds partial s's (m, l); lane c owns channels c, c + 64, ... and loads all NS
+// partial rows of them before using any (rows past S re-read row S - 1 and get weight 0), so the
+// merge is one memory round trip; each weight reaches the other lanes by v_readlane. Workgroup b
+// takes KV head b % n_kv, as decode_merge_kernel does.
+template <int D, int G, int NS>
+__global__ __launch_bounds__(64) void decode_merge_wave_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_o,
+                                                               int S, void* __restrict__ out, int out_dtype, float* __restrict__ lse) {
+  static_assert(NS <= 64 && D % 64 == 0, "a lane per partial, whole rows of 64 channels");
+  constexpr int kC = D / 64;
+  const int n_kv = gridDim.x / G;
+  const int h = blockIdx.x % n_kv, j = blockIdx.x / n_kv;
+  const int row = h * G + j;
+  const int lane = threadIdx.x;
+  const float* o = part_o + (int64_t)h * S * G * D + (int64_t)j * D + lane;
+  float v[NS][kC];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int c = 0; c < kC; ++c) v[s][c] = o[(int64_t)min(s, S - 1) * G * D + 64 * c];
+  const float2 mlp = *(const float2*)(part_ml + ((int64_t)h * S * G + (int64_t)min(lane, S - 1) * G + j) * 2);
+  const float m_t = lane < S ? mlp.x : -INFINITY;
+  const float M = lkv::wave_max_f32(m_t);
+  const bool any = M != -INFINITY;
+  const float w_t = (lane < S && any) ? exp2f(m_t - M) : 0.0f;
+  const float L = lkv::wave_sum_f32(lane < S ? mlp.y * w_t : 0.0f);
+  float acc[kC];
+#pragma unroll
+  for (int c = 0; c < kC; ++c) acc[c] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_t), s));
+#pragma unroll
+    for (int c = 0; c < kC; ++c) acc[c] += v[s][c] * w;
+  }
+#pragma unroll
+  for (int c = 0; c < kC; ++c) lkv::store_any(out, (int64_t)row * D + 64 * c + lane, out_dtype, L > 0.0f ? acc[c] / L : 0.0f);
+  if (lane == 0) lse[row] = (!any || !(L > 0.0f)) ? -INFINITY : (M + log2f(L)) * lkv::kLn2;
+}
+
 struct Plan {
   int n_a, per_a, splits_a, per_b, splits_b;
   int nt = kThreads;  // workgroup size of the launch
@@ -1314,8 +1354,16 @@ int launch(hipStream_t stream, DecodeArgs& a) {
                  : a.n_cand <= 2 * kSelUnit ? launch_inst<D, MT, G, 2>(stream, a, inst)
                                             : launch_inst<D, MT, G, 4>(stream, a, inst);
   if (rc != LKV_OK) return rc;
-  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(512), 0, stream, a.part_ml, a.part_o, S,
-                     a.out, a.out_dtype, a.lse);
+  if (S <= 32) {
+    hipLaunchKernelGGL((decode_merge_wave_kernel<D, G, 32>), dim3(a.n_kv * G), dim3(64), 0, stream, a.part_ml, a.part_o, S, a.out,
+                       a.out_dtype, a.lse);
+  } else if (S <= 64) {
+    hipLaunchKernelGGL((decode_merge_wave_kernel<D, G, 64>), dim3(a.n_kv * G), dim3(64), 0, stream, a.part_ml, a.part_o, S, a.out,
+                       a.out_dtype, a.lse);
+  } else {
+    hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.n_kv * G), dim3(512), 0, stream, a.part_ml, a.part_o, S, a.out,
+                       a.out_dtype, a.lse);
+  }
   LKV_CHECK_LAUNCH("decode_merge");
   return LKV_OK;
 }
