@@ -265,9 +265,9 @@ def step_kernels(fused: bool, in_decode: bool, n_cand: int) -> str:
     12,288 and select_stream_kernel beyond."""
     call = "one lkv_select_decode call: " if fused else "lkv_bound_topk + lkv_sparse_decode: "
     if fused and in_decode:
-        return call + "bound_kernel_mf, sparse_decode_kernel choosing the top K itself, decode_merge_kernel"
+        return call + "bound_kernel_mf, sparse_decode_kernel choosing the top K itself, decode_merge_wave_kernel"
     sel = "select_block_kernel" if n_cand <= 8192 else ("select_kernel" if n_cand <= 12288 else "select_stream_kernel")
-    return call + f"bound_kernel_mf, {sel}, sparse_decode_kernel, decode_merge_kernel"
+    return call + f"bound_kernel_mf, {sel}, sparse_decode_kernel, decode_merge_wave_kernel"
 
 
 def pmc_traffic(workload: str) -> dict:
@@ -593,7 +593,9 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
         "host_syncs_per_layer": 0,
         "step_stats": dict(m["step_stats"], note="each step replayed between events of its own, after the timed region"),
     }
-    # The dominant kernel is lkv_sparse_decode (sparse_decode_kernel + decode_merge_kernel).
+    # The dominant kernel is lkv_sparse_decode: sparse_decode_kernel and its merge launch (the one-wave
+    # merge up to 64 partials per head; the exact split's 100-odd partials take decode_merge_kernel).
+    merge = "decode_merge_kernel" if kind == "exact" else "decode_merge_wave_kernel"
     traffic = pmc_traffic(args.workload)
     traffic_note = {}
     if traffic.get(f"{main_leg}/sparse_decode_kernel"):
@@ -602,8 +604,8 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
                         "traffic_run": pmc_run(args.workload, main_leg)}
     if m["sparse_decode_pcie_bytes"]:
         gbps = m["sparse_decode_pcie_gbps"]
-        kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H))
-                 else "sparse_decode_kernel + decode_merge_kernel")
+        kname = (f"sparse_decode_kernel (top-K inside) + {merge}" if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H))
+                 else f"sparse_decode_kernel + {merge}")
         out["roofline"] = {"bound": "pcie", "kernel": f"{kname}, host reads over PCIe", "achieved": gbps,
                            "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / PCIE_PEAK_GBPS, 4), "traffic": traffic.get(f"{main_leg}/sparse_decode_kernel"),
                            "algorithmic_bytes": m["sparse_decode_pcie_bytes"], "kernel_us": m["sparse_decode_us"], **traffic_note}
@@ -612,8 +614,8 @@ def run_decode(args: argparse.Namespace, spec: dict) -> dict:
             out["roofline"]["frac_of_link_ceiling"] = round(gbps / probe["dma_h2d_gbps"], 4)
     else:
         gbps = m["sparse_decode_hbm_gbps"]
-        kname = ("sparse_decode_kernel (top-K inside) + decode_merge_kernel" if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H))
-                 else "sparse_decode_kernel + decode_merge_kernel")
+        kname = (f"sparse_decode_kernel (top-K inside) + {merge}" if (m["fused"] and kernels._lib.selects_in_decode(n_cand, res[main_leg]["host_sel"], N_Q // H))
+                 else f"sparse_decode_kernel + {merge}")
         out["roofline"] = {"bound": "hbm", "kernel": f"{kname}, HBM", "achieved": gbps,
                            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic.get(f"{main_leg}/sparse_decode_kernel"),
                            "algorithmic_bytes": m["sparse_decode_hbm_bytes"], "kernel_us": m["sparse_decode_us"], **traffic_note}
@@ -823,7 +825,7 @@ def run_hybrid(args: argparse.Namespace, spec: dict) -> dict:
     log(f"hybrid128k: hybrid {warm_h:.1f} us/layer (cold step {t_h[0]:.1f}), zero-copy {warm_z:.1f} us/layer, hit rate {hit_rate:.3f}")
     step_gbps = miss_bytes / (warm_h * 1e-6) / 1e9
     roofline = {"bound": "pcie", "kernel": "the whole lkv_select_hybrid_decode call per layer (bound_kernel_mf, residency_kernel choosing the top K, "
-                                            "sparse_decode_kernel reading hits from HBM slots and misses over PCIe, decode_merge_kernel)",
+                                            "sparse_decode_kernel reading hits from HBM slots and misses over PCIe, decode_merge_wave_kernel)",
                 "achieved": round(step_gbps, 2), "peak": PCIE_PEAK_GBPS, "unit": "GB/s", "frac": round(step_gbps / PCIE_PEAK_GBPS, 4), "traffic": None,
                 "algorithmic_bytes": int(miss_bytes), "step_us": round(warm_h, 2),
                 "note": "the missed pairs' host bytes per layer over the warm steps' mean call time, launches and gaps included; the call is "

@@ -62,7 +62,7 @@ def kernels() -> list[dict]:
 
 def test_every_kernel_of_the_path_is_in_the_library(kernels) -> None:  # noqa: ANN001
     names = " ".join(k[".name"] for k in kernels)
-    for want in ("bound_kernel", "select_kernel", "select_stream_kernel", "sparse_decode_kernel", "decode_merge_kernel",
+    for want in ("bound_kernel", "select_kernel", "select_stream_kernel", "sparse_decode_kernel", "decode_merge_kernel", "decode_merge_wave_kernel",
                  "residency_kernel", "store_blocks_kernel", "merge_lse_kernel", "stream_read_kernel"):
         assert want in names, want
 
