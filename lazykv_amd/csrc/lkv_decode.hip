@@ -1207,11 +1207,7 @@ struct Plan {
 struct PlanHints {
   bool sel_host = false, rem_host = false;
   size_t sel_pair = 0, rem_pair = 0;
-  bool hybrid = false;  // the selected pairs are read from HBM slots where resident, from the host pool otherwise
 };
-#ifndef LKV_HYBRID_READ_SCALE
-#define LKV_HYBRID_READ_SCALE 3
-#endif
 
 constexpr int kHostMinWgs = 64;  // floor on the workgroups of a launch that reads selected pairs from host memory
 
@@ -1270,7 +1266,7 @@ static Plan make_plan(const lkv_decode_desc* d, const PlanHints& hint = PlanHint
     // bytes in flight: 8 workgroups per head gave 615-619 us/layer at 16-, 32- and 64-token
     // blocks, 4 per head 641-645 at each of them, and 1 per head (64-token blocks) 652, under
     // read budgets of 1-8 MiB.
-    int s = host_splits(hint.sel_pair, d->n_kv, lkv_host_read_inflight() * (hint.hybrid ? LKV_HYBRID_READ_SCALE : 1));
+    int s = host_splits(hint.sel_pair, d->n_kv, lkv_host_read_inflight());
     const int floor_s = (kHostMinWgs + d->n_kv - 1) / d->n_kv;
     if (s < floor_s) s = floor_s;
     if (s < p.splits_a) {
@@ -1808,7 +1804,6 @@ static int sparse_decode_impl(uintptr_t stream, const lkv_decode_desc* desc, con
                   (long long)rem->n_blocks);
   }
   PlanHints hint;
-  hint.hybrid = res != nullptr;
   if (attend_sel) {
     hint.sel_host = (sel->flags & LKV_SRC_HOST) != 0;
     hint.sel_pair = lkv_pair_bytes(sel, d.block_size, d.head_dim);

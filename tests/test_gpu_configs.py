@@ -185,6 +185,45 @@ def test_zero_copy_decode_128k_bfloat16_k512() -> None:
     assert np.abs(lse - want_l).max() < TOL
 
 
+@pytest.mark.parametrize("quant", [None, "int8"])
+def test_hybrid_residency_128k_bfloat16_k512_is_the_zero_copy_step(quant: str | None) -> None:
+    """The hybrid step at the 8B shape (131,072 tokens, K 512 of 8,190, 512 slots per head, bf16
+    pairs or int8 records in host memory) over three drifting queries -- the first with empty
+    slots, the others with hits and misses -- chooses the zero-copy step's ids and gives its
+    output and LSE bit for bit: the decode launch takes the zero-copy plan, and a hit reads from
+    its slot exactly what the miss wrote there."""
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+
+    int8 = quant == "int8"
+    layer = _Layer(128, 131072, torch.bfloat16, int8=int8, meta_from="dequantised" if int8 else "exact")
+    src = layer.records if int8 else layer.pool
+    host = pinned_empty(tuple(src.shape), src.dtype)
+    host.copy_(src)
+    hs = kernels.record_source(host, torch.bfloat16) if int8 else kernels.pool_source(host)
+    res = kernels.Residency.allocate(512, H, layer.n, BS, 128, torch.bfloat16, torch.device("cuda"))
+    slots = layer.pool[[0, layer.n_sealed]].contiguous()
+    ss = kernels.pool_source(slots)
+    common = dict(cand_offset=1, n_cand=layer.n_sealed - 1, block_size=BS, scale=128**-0.5, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=layer.fill,
+                  out_dtype=torch.float32)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    base = layer.q.float()
+    rms = base.pow(2).mean(dim=-1, keepdim=True).sqrt()
+    hits = []
+    for step in range(3):
+        q = (base + 0.25 * rms * torch.randn(base.shape, generator=gen, device="cuda")).to(torch.bfloat16)
+        before = res.block_slot.clone()
+        ih = torch.empty((H, 512), dtype=torch.int32, device="cuda")
+        iz = torch.empty_like(ih)
+        oh, lh = kernels.select_hybrid_decode(q, layer.kmin, layer.kmax, 512, host=hs, res=res, out_idx=ih, **common)
+        oz, lz = kernels.select_decode(q, layer.kmin, layer.kmax, 512, sel=hs, out_idx=iz, **common)
+        torch.cuda.synchronize()
+        assert torch.equal(ih, iz), step
+        assert torch.equal(oh, oz) and torch.equal(lh, lz), step
+        hits.append(int((torch.gather(before, 1, ih.long()) >= 0).sum()))
+    assert hits[0] == 0 and all(0 < x < H * 512 for x in hits[1:]), hits
+
+
 @pytest.fixture(scope="module")
 def exact_layer():  # noqa: ANN201
     from lazykv_amd.pinned import pinned_empty
