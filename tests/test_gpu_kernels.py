@@ -345,6 +345,32 @@ def test_sparse_decode_matches_the_oracle(where: str, h: int, g: int, n: int, d:
     assert torch.equal(out_bf, out.to(torch.bfloat16)) and torch.equal(lse_bf, lse)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("k", [6, 254, 262, 510, 518, 1022])
+def test_merge_folds_any_number_of_partials(d: int, k: int) -> None:
+    """The merge launch over 1, 32, 33, 64, 65 and 128 partials per head (2 KV heads: the HBM plan
+    splits a head's k + 2 items into runs of 8 over 128 workgroups), across the one-wave merge's
+    limits of 32 and 64 partials and into the 512-thread merge beyond: output and LSE match the
+    oracle, and the model-dtype output is the float32 one rounded."""
+    from lazykv_amd import kernels
+
+    h, g, bs, fill = 2, 4, 16, 11
+    n = k + 10
+    w, pool = _pool_case(k + d, h, g, n, bs, d, torch.bfloat16)
+    gen = torch.Generator().manual_seed(k)
+    chosen = torch.stack([torch.randperm(n - 2, generator=gen)[:k] + 1 for _ in range(h)]).to(torch.int32)
+    src = kernels.pool_source(pool.cuda())
+    scale = d**-0.5
+    args = dict(n_kv=h, block_size=bs, scale=scale, sel=src, idx=chosen.cuda(), sink=src, sink_block=0, cur=src, cur_block=n - 1, fill=fill)
+    out, lse = kernels.sparse_decode(w.query.cuda(), out_dtype=torch.float32, **args)
+    out_bf, lse_bf = kernels.sparse_decode(w.query.cuda(), **args)
+    torch.cuda.synchronize()
+    want_o, want_l = _oracle_decode(w.query, _f64(pool), chosen.numpy(), 0, n - 1, fill, scale, bs)
+    assert np.abs(out.cpu().numpy() - want_o).max() < TOL
+    assert np.abs(lse.cpu().numpy() - want_l).max() < TOL
+    assert torch.equal(out_bf, out.to(torch.bfloat16)) and torch.equal(lse_bf, lse)
+
+
 @pytest.mark.parametrize("bs", [32, 64, 128])
 def test_host_reads_of_large_blocks_take_the_workgroup_floor_and_match_the_oracle(bs: int) -> None:
     """Selected pairs of 16-64 KiB read from host memory: the read budget alone would give 1-4
