@@ -346,15 +346,16 @@ def test_sparse_decode_matches_the_oracle(where: str, h: int, g: int, n: int, d:
 
 
 @pytest.mark.parametrize("d", [64, 128])
-@pytest.mark.parametrize("k", [6, 254, 262, 510, 518, 1022])
-def test_merge_folds_any_number_of_partials(d: int, k: int) -> None:
-    """The merge launch over 1, 32, 33, 64, 65 and 128 partials per head (2 KV heads: the HBM plan
-    splits a head's k + 2 items into runs of 8 over 128 workgroups), across the one-wave merge's
-    limits of 32 and 64 partials and into the 512-thread merge beyond: output and LSE match the
-    oracle, and the model-dtype output is the float32 one rounded."""
+@pytest.mark.parametrize(("g", "k"), [(4, 6), (4, 254), (4, 262), (4, 510), (4, 518), (4, 1022), (8, 254), (8, 510), (8, 1022)])
+def test_merge_folds_any_number_of_partials(d: int, g: int, k: int) -> None:
+    """The merge launch over 1, 32, 33, 64, 65 and 128 partials per head (2 KV heads, 4 query heads
+    each: the HBM plan splits a head's k + 2 items into runs of 8 over 128 workgroups), across the
+    one-wave merge's limits of 32 and 64 partials and into the 512-thread merge beyond; with 8 query
+    heads per KV head (the 4-wave plan: at most 64 partials, 32 and 64 here) the G = 8 merges.
+    Output and LSE match the oracle, and the model-dtype output is the float32 one rounded."""
     from lazykv_amd import kernels
 
-    h, g, bs, fill = 2, 4, 16, 11
+    h, bs, fill = 2, 16, 11
     n = k + 10
     w, pool = _pool_case(k + d, h, g, n, bs, d, torch.bfloat16)
     gen = torch.Generator().manual_seed(k)
