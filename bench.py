@@ -68,8 +68,8 @@ def main() -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--workload", choices=sorted(WORKLOADS), default="decode128k")
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--layers", type=int, default=None)
     p.add_argument("--tokens", type=int, default=None)
     p.add_argument("--k", type=int, default=None, help="selected blocks per KV head (default: the workload's)")
