@@ -837,6 +837,65 @@ __device__ __forceinline__ void attend_fill_i8(const DecodeArgs& a, int block, i
   }
 }
 
+// One selected item of a hybrid launch: the pair it reads (its slot for a hit; the host pool for a
+// miss, whose pair is also written into its slot) and whether it is attended at all.
+struct HybridItem {
+  bool ok, miss;
+  int blk, slot;
+};
+__device__ __forceinline__ HybridItem hybrid_item(const DecodeArgs& a, const int32_t* idx_h, int sel_base, int h, int j, int je) {
+  HybridItem it{false, false, 0, 0};
+  if (j >= je) return it;
+  const int32_t l = a.loc[(int64_t)h * a.loc_stride + j];
+  if (l < 0) return it;
+  if (l & kLocMiss) {
+    const int b = idx_h[j - sel_base], sl = l & ~kLocMiss;
+    it.ok = b >= 0 && (int64_t)b < a.sel.nblk && (int64_t)sl < a.slots.nblk;
+    it.miss = true;
+    it.blk = b;
+    it.slot = sl;
+  } else {
+    it.ok = (int64_t)l < a.slots.nblk;
+    it.blk = it.slot = l;
+  }
+  return it;
+}
+
+// The selected items of a hybrid launch over a model-dtype host pool with blocks of at most 16
+// tokens (one chunk a pair): each wave issues its next item's loads before it folds the current
+// one, so a miss read over the link overlaps the item after it. The items, the pair each reads,
+// the slot a miss writes and the order they are folded in are those of the one-pair loop
+// (attend_fill, attend_two), so the results are identical. Every load is issued unconditionally --
+// an item that is not attended reads slot 0 and is not folded -- so the waits stay counts of the
+// loads issued after a pair's, and the next pair's loads stay in flight.
+template <int D, int MT, int G, int NW>
+__device__ __forceinline__ void attend_hybrid_piped(const DecodeArgs& a, const int32_t* idx_h, int sel_base, int js, int je, int wave, int h,
+                                                    const float (&q)[G][Lanes<D>::EPL], int r, int c, WaveState<D, G>& st) {
+  using L = Lanes<D>;
+  const int nit = min(L::NI, (a.bs + L::RG - 1) / L::RG);
+  const int j0 = js + __builtin_amdgcn_readfirstlane(wave);
+  auto issue = [&](const HybridItem& it, RawModel<D, MT>& raw) {
+    load_raw<D, MT>((it.ok && it.miss) ? a.sel : a.slots, it.ok ? it.blk : 0, h, 0, nit, a.bs, r, c, raw);
+  };
+  auto fold = [&](const HybridItem& it, RawModel<D, MT>& raw) {
+    if (!it.ok) return;  // wave-uniform
+    if (it.miss) store_raw<D, MT>(a.slots, it.slot, h, 0, nit, a.bs, r, c, raw);
+    consume_chunk<D, G>(q, Widen<D, MT>(raw), raw, 0, nit, a.bs, r, st);
+  };
+  RawModel<D, MT> ra, rb;
+  HybridItem ia = hybrid_item(a, idx_h, sel_base, h, j0, je);
+  issue(ia, ra);
+  for (int j = j0; j < je; j += 2 * NW) {
+    const HybridItem ib = hybrid_item(a, idx_h, sel_base, h, j + NW, je);
+    issue(ib, rb);
+    fold(ia, ra);
+    if (j + NW >= je) break;
+    ia = hybrid_item(a, idx_h, sel_base, h, j + 2 * NW, je);
+    issue(ia, ra);
+    fold(ib, rb);
+  }
+}
+
 // Candidates a fused-selection workgroup holds (KPT keys per thread): SEL * kSelUnit per KV head.
 // SEL 1 holds 2,048 (a 32,768-token context at 16-token blocks), SEL 2 holds 4,096, SEL 4 holds
 // 8,192; a launch takes the smallest that fits, since every key slot a thread holds costs its
@@ -960,10 +1019,16 @@ __global__ __launch_bounds__(NT) void sparse_decode_kernel(DecodeArgs a) {
       // 16-row chunks).
       constexpr bool HYB = I8 && NT == kThreads && SEL == 0;
       constexpr int NPA = ((I8 && NT == kThreads) || MT == LKV_F32) ? 1 : 2;
-      bool piped = false;  // the selected pairs were attended four per round
+      bool piped = false;  // the selected pairs were attended by a pipelined loop
       if constexpr (I8 && NT == kThreadsHbm && NPA == 2) {
         if (a.sel.dtype == LKV_INT8_RECORD && a.bs <= 16) {
           attend_selected_i8_four<D, MT, G, NW, (SEL > 0)>(a, idx_h, sel_base, js, je, wave, h, q, r, c, st);
+          piped = true;
+        }
+      }
+      if constexpr (HYB) {
+        if (a.loc != nullptr && a.sel.dtype != LKV_INT8_RECORD && a.bs <= 16) {
+          attend_hybrid_piped<D, MT, G, NW>(a, idx_h, sel_base, js, je, wave, h, q, r, c, st);
           piped = true;
         }
       }
