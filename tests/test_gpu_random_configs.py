@@ -8,7 +8,9 @@ hand-picked cases do not: 4- and 8-wave workgroups, the matrix-core and vector i
 three pairs per step, chunked and short blocks. Bars as elsewhere: float32 output and LSE within
 2e-3 of the float64 oracle. A second sweep draws bound + top-K calls (candidate counts on both
 sides of the in-register limit, offsets, sorted and ascending output): the float32 bounds within
-the accumulation error bound of the float64 ones, the selected sets under the near-tie rule.
+the accumulation error bound of the float64 ones, the selected sets under the near-tie rule. A
+third draws hybrid residency configurations over drifting steps: bit-identical to the zero-copy
+decode, tables and use order equal to the oracle's.
 """
 
 from __future__ import annotations
@@ -233,3 +235,79 @@ def test_random_block_store_matches_the_oracle(seed: int) -> None:
     mx = kmax[0].cpu().double().numpy().transpose(1, 0, 2)
     assert np.array_equal(mn[rng_b], stored_keys.min(axis=2)) and np.array_equal(mx[rng_b], stored_keys.max(axis=2))
     assert not mn[:first].any() and not mn[first + count :].any()
+
+
+N_HYBRID = 24
+
+
+def _hybrid_case(seed: int) -> dict:
+    rng = np.random.default_rng(5000 + seed)
+    bs = int(rng.choice([4, 8, 16, 16, 16, 32, 64]))
+    n = int(rng.integers(24, max(25, 2048 // bs)))
+    k = int(rng.integers(1, min(n - 2, 600)))
+    return {
+        "h": int(rng.choice([1, 2, 4, 8])),
+        "g": int(rng.choice([1, 2, 4, 8])),
+        "d": int(rng.choice([64, 128])),
+        "bs": bs,
+        "n": n,
+        "k": k,
+        "spare": int(rng.choice([0, 0, int(rng.integers(1, k + 2))])),
+        "fill": int(rng.integers(1, bs + 1)),
+        "dt": [torch.float16, torch.bfloat16][int(rng.integers(0, 2))],
+        "int8": bool(rng.random() < 0.4),
+    }
+
+
+@pytest.mark.parametrize("seed", range(N_HYBRID))
+def test_random_hybrid_configuration_is_the_zero_copy_decode(seed: int) -> None:
+    """Seeded random hybrid configurations (KV heads, group size, head_dim, block size -- the
+    pipelined item loop for model-dtype pools of blocks up to 16 tokens, the one-pair loop
+    otherwise --, budget, spare slots, dtype, bf16/f16 pairs or int8 records) over five drifting
+    steps: output and LSE equal the zero-copy decode's bit for bit, the tables and use order equal
+    the oracle's, and every occupied slot holds its block as a decode reads it."""
+    from lazykv_amd import kernels
+    from lazykv_amd.pinned import pinned_empty
+    from lazykv_amd.workload import draw_layer, to_pool
+
+    c = _hybrid_case(seed)
+    h, g, d, bs, n, k, dt = c["h"], c["g"], c["d"], c["bs"], c["n"], c["k"], c["dt"]
+    print(f"hybrid case {seed}: {c}", flush=True)
+    w = draw_layer(seed, h * g, h, d, n * bs, bs, dt)
+    pool = to_pool(w.keys, w.values, bs).cuda()
+    kmin = torch.zeros((1, h, n, d), dtype=dt, device="cuda")
+    kmax = torch.zeros_like(kmin)
+    kernels.store_blocks(kernels.dense_source(w.keys.cuda(), w.values.cuda(), bs), n_kv=h, head_dim=d, block_size=bs, first_block=0, n_blocks=n - 1,
+                         kmin=kmin, kmax=kmax)
+    expect = pool
+    if c["int8"]:
+        recs = kernels.pack_int8(pool.reshape(n * h, 2, bs, d))
+        expect = kernels.unpack_int8(recs, bs, d, dt).reshape(n, h, 2, bs, d)
+        host = pinned_empty((n, h, recs.shape[1]), torch.uint8)
+        host.copy_(recs.reshape(n, h, -1))
+        hsrc = kernels.record_source(host, dt)
+    else:
+        host = pinned_empty(tuple(pool.shape), dt)
+        host.copy_(pool)
+        hsrc = kernels.pool_source(host)
+    n_slots = k + c["spare"]
+    res = kernels.Residency.allocate(k, h, n, bs, d, dt, torch.device("cuda"), n_slots=n_slots)
+    tb, ts, tl = R.residency_state(h, n_slots, n)
+    ss = kernels.pool_source(pool[[0, n - 1]].contiguous())
+    gen = torch.Generator().manual_seed(seed)
+    q0 = w.query.float()
+    for step in range(5):
+        q = (q0 + 0.35 * torch.randn(q0.shape, generator=gen)).to(dt).cuda()
+        idx = kernels.bound_topk(q, kmin, kmax, k, cand_offset=1, n_cand=n - 2)
+        common = dict(n_kv=h, block_size=bs, scale=d**-0.5, idx=idx, sink=ss, sink_block=0, cur=ss, cur_block=1, fill=c["fill"], out_dtype=torch.float32)
+        out_z, lse_z = kernels.sparse_decode(q, sel=hsrc, **common)
+        out_h, lse_h = kernels.hybrid_decode(q, host=hsrc, res=res, **common)
+        torch.cuda.synchronize()
+        assert torch.equal(out_h, out_z) and torch.equal(lse_h, lse_z), step
+        R.residency_step(tb, ts, tl, idx.cpu().numpy().astype(np.int64), step)
+        assert np.array_equal(res.block_slot.cpu().numpy(), tb), step
+        assert np.array_equal(res.slot_block.cpu().numpy(), ts), step
+        assert np.array_equal(res.order.cpu().numpy(), R.slot_order(tl)), step
+        for j in range(h):
+            held = np.flatnonzero(ts[j] >= 0)
+            assert torch.equal(res.slots[torch.from_numpy(held).cuda(), j], expect[torch.from_numpy(ts[j, held]).cuda(), j]), (step, j)
